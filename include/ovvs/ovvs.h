@@ -1,0 +1,178 @@
+/* libovvs — MI355X (gfx950) implementation of the ovVS IVF-PQ search path.
+ *
+ * This header declares the subset of the reference C ABI that reaches IVF-PQ
+ * (reference include/ovvs/ovvs.h:11-121,165-214,276-286,406) with identical enum
+ * values, struct layouts, symbol names and signatures, so the reference's C,
+ * C++ (ovvs.hpp) and Python ctypes callers bind to libovvs.so unchanged.
+ * Every computation behind these entry points runs on the GPU; there is no CPU
+ * route. Entry points marked ADDITIVE have no reference counterpart.
+ *
+ * Pointers are host memory unless the entry point says "device". */
+#pragma once
+
+#include "export.h"
+#include "status.h"
+#include "version.h"
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* reference include/ovvs/ovvs.h:13-19 */
+typedef enum ovvsDevice {
+  OVVS_DEVICE_AUTO = 0,
+  OVVS_DEVICE_CPU = 1,
+  OVVS_DEVICE_NPU = 2,
+  OVVS_DEVICE_GPU = 3,
+  OVVS_DEVICE_HETERO = 4
+} ovvsDevice;
+
+/* reference include/ovvs/ovvs.h:21-29. Every non-forced policy and FORCE_GPU run
+ * on the GPU. FORCE_CPU and FORCE_NPU name devices this library does not drive
+ * and make compute entry points return OVVS_STATUS_DEVICE_UNAVAILABLE. */
+typedef enum ovvsPolicy {
+  OVVS_POLICY_AUTO = 0,
+  OVVS_POLICY_NPU_IF_FASTER = 1,
+  OVVS_POLICY_GPU_IF_FASTER = 2,
+  OVVS_POLICY_HETERO = 3,
+  OVVS_POLICY_FORCE_NPU = 4,
+  OVVS_POLICY_FORCE_GPU = 5,
+  OVVS_POLICY_FORCE_CPU = 6
+} ovvsPolicy;
+
+/* reference include/ovvs/ovvs.h:31-38. The metric only changes the exact
+ * re-rank; the coarse probe and the lookup tables are always L2. */
+typedef enum ovvsMetric {
+  OVVS_METRIC_L2_EXPANDED = 0,
+  OVVS_METRIC_L2_SQRT_EXPANDED = 1,
+  OVVS_METRIC_INNER_PRODUCT = 2,
+  OVVS_METRIC_COSINE_EXPANDED = 3,
+  OVVS_METRIC_BITWISE_HAMMING = 4,
+  OVVS_METRIC_LP_UNEXPANDED = 5
+} ovvsMetric;
+
+/* reference include/ovvs/ovvs.h:40-48 */
+typedef enum ovvsDType {
+  OVVS_DTYPE_F32 = 0,
+  OVVS_DTYPE_F16 = 1,
+  OVVS_DTYPE_I8 = 2,
+  OVVS_DTYPE_U8 = 3,
+  OVVS_DTYPE_F8E4M3 = 4,
+  OVVS_DTYPE_F8E5M2 = 5,
+  OVVS_DTYPE_F4E2M1 = 6
+} ovvsDType;
+
+/* Opaque handles (reference include/ovvs/ovvs.h:77,80). */
+typedef struct ovvsResourcesImpl* ovvsResources_t;
+typedef struct ovvsIvfPqIndexImpl* ovvsIvfPqIndex_t;
+
+#define OVVS_IVF_PQ_SEARCH_STATS_ABI_V1 1u
+
+/* Cumulative telemetry of successful IVF-PQ searches on one Resources object.
+ * Frozen 200-byte layout (reference include/ovvs/ovvs.h:89-121); counters
+ * saturate at INT64_MAX. Stage times come from HIP events on the Resources
+ * stream: coarse_pairwise_ns is the coarse distance kernel, coarse_topk_ns the
+ * probe selection, adc_scan_select_ns the fused LUT-build + code-scan +
+ * shortlist kernel (lut_build_ns stays 0 because the LUT is built inside that
+ * kernel), refine_distance_ns the fused gather + exact distance + final select
+ * kernel. candidate_rows counts every (query, probed list) row scanned, so
+ * candidate_rows * pq_m is the algorithmic code-byte volume. */
+typedef struct ovvsIvfPqSearchStatsV1 {
+  uint32_t abi_version;
+  uint32_t struct_size;
+  int64_t successful_calls;
+  int64_t blocks;
+  int64_t queries;
+  int64_t tasks;
+  int64_t candidate_rows;
+  int64_t selected_rows;
+  int64_t total_wall_ns;
+  int64_t coarse_pairwise_ns;
+  int64_t coarse_topk_ns;
+  int64_t planning_ns;
+  int64_t lut_build_ns;
+  int64_t adc_scan_select_ns;
+  int64_t shortlist_select_validate_ns;
+  int64_t refine_gather_ns;
+  int64_t refine_distance_ns;
+  int64_t refine_topk_ns;
+  int64_t gpu_allocation_calls;
+  int64_t gpu_allocation_bytes;
+  int64_t gpu_h2d_calls;
+  int64_t gpu_h2d_bytes;
+  int64_t gpu_d2h_calls;
+  int64_t gpu_d2h_bytes;
+  int64_t gpu_kernel_launches;
+  int64_t gpu_wait_calls;
+} ovvsIvfPqSearchStatsV1;
+
+/* Concurrency (reference include/ovvs/ovvs.h:165-166): concurrent searches may
+ * share one immutable index when each thread uses its own Resources. Each
+ * Resources owns one HIP stream and one device workspace. Do not mutate,
+ * serialize or destroy an index while it is being searched. */
+
+/* reference include/ovvs/ovvs.h:171-172 */
+OVVS_API const char* ovvsGetVersion(void);
+OVVS_API const char* ovvsStatusString(ovvsStatus status);
+
+/* reference include/ovvs/ovvs.h:174-184,210-211. Creating Resources does not
+ * touch the GPU; the device is opened on first use. */
+OVVS_API ovvsStatus ovvsResourcesCreate(ovvsResources_t* res);
+OVVS_API ovvsStatus ovvsResourcesDestroy(ovvsResources_t res);
+OVVS_API ovvsStatus ovvsResourcesSetPolicy(ovvsResources_t res, ovvsPolicy policy);
+OVVS_API ovvsStatus ovvsResourcesGetPolicy(ovvsResources_t res, ovvsPolicy* policy);
+OVVS_API ovvsStatus ovvsResourcesNpuAvailable(ovvsResources_t res, int32_t* available);
+OVVS_API ovvsStatus ovvsResourcesGpuAvailable(ovvsResources_t res, int32_t* available);
+OVVS_API ovvsStatus ovvsResourcesSku(ovvsResources_t res, char* buf, int32_t len);
+OVVS_API ovvsStatus ovvsResourcesLastDevice(ovvsResources_t res, ovvsDevice* device);
+OVVS_API ovvsStatus ovvsResourcesLastComputeDtype(ovvsResources_t res, ovvsDType* dtype);
+OVVS_API ovvsStatus ovvsResourcesIvfPqSearchStatsV1(ovvsResources_t res,
+                                                    ovvsIvfPqSearchStatsV1* stats);
+
+/* IVF-PQ (reference include/ovvs/ovvs.h:276-286). */
+OVVS_API ovvsStatus ovvsIvfPqBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                   int64_t dim, ovvsMetric metric, int32_t nlist, int32_t pq_m,
+                                   int32_t pq_nbits, ovvsIvfPqIndex_t* index);
+OVVS_API ovvsStatus ovvsIvfPqSearch(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                    const float* queries, int64_t nq, int64_t k, int32_t nprobe,
+                                    int32_t krefine, const uint8_t* bitset, int64_t* neighbors,
+                                    float* distances);
+OVVS_API ovvsStatus ovvsIvfPqSerialize(ovvsIvfPqIndex_t index, const char* path);
+OVVS_API ovvsStatus ovvsIvfPqDeserialize(ovvsResources_t res, const char* path,
+                                         ovvsIvfPqIndex_t* index);
+OVVS_API ovvsStatus ovvsIvfPqExtend(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                    const float* extra, int64_t nextra);
+OVVS_API ovvsStatus ovvsIvfPqDestroy(ovvsIvfPqIndex_t index);
+
+/* ADDITIVE (no reference counterpart; the reference builds fp32 tables only).
+ * ovvsIvfPqSearch with a choice of lookup-table precision: lut_dtype is
+ * OVVS_DTYPE_F32 (identical to ovvsIvfPqSearch) or OVVS_DTYPE_F16 (each fp32
+ * table entry rounded to binary16, round-to-nearest-even, overflow to +inf;
+ * sums stay fp32). Any other dtype returns OVVS_STATUS_UNSUPPORTED. */
+OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                      const float* queries, int64_t nq, int64_t k,
+                                      int32_t nprobe, int32_t krefine, const uint8_t* bitset,
+                                      ovvsDType lut_dtype, int64_t* neighbors,
+                                      float* distances);
+
+/* ADDITIVE (no reference counterpart). Same search with every buffer already
+ * in device memory of the current HIP device: queries [nq*dim] f32, bitset
+ * ((n+7)/8 bytes, may be NULL), neighbors [nq*k] i64, distances [nq*k] f32.
+ * Returns after the results are complete. For callers that keep queries and
+ * results resident in HBM (no PCIe copies on the search path). */
+OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                          const float* queries, int64_t nq, int64_t k,
+                                          int32_t nprobe, int32_t krefine,
+                                          const uint8_t* bitset, ovvsDType lut_dtype,
+                                          int64_t* neighbors, float* distances);
+
+/* Allow-list to an LSB-first bitset of (n+7)/8 bytes; ids outside [0,n) are
+ * ignored (reference include/ovvs/ovvs.h:406, src/rt/resources.cpp:218-229). */
+OVVS_API ovvsStatus ovvsBitsetFromAllowList(int64_t n, const int64_t* ids, int64_t nids,
+                                            uint8_t* bitset);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,276 @@
+"""Python handles on the CPU parity checkers (test infrastructure only).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module; libovvs never does.
+
+* ``Oracle``  — our C restatement of the reference search (oracle/ivfpq_oracle.c,
+  built into oracle/liboracle.so).
+* ``Reference`` — the reference library itself, compiled from /root/reference by
+  ``make -C oracle ref`` into oracle/_ref/libovvs_ref.so, driven through its own C
+  ABI with the FORCE_CPU policy (its CPU route, reference
+  src/neighbors/indexes.cpp:538-1134).
+* ``read_ipq1`` — parses an IPQ1 v1 file (reference src/neighbors/indexes.cpp:1141-1178)
+  into the list-major arrays both searchers consume.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_uint8, c_uint16, c_void_p
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libovvs_ref.so"
+
+FORCE_CPU = 6
+
+
+@dataclass
+class Ipq1:
+    n: int
+    dim: int
+    nlist: int
+    pq_m: int
+    pq_ks: int
+    dsub: int
+    metric: int
+    centroids: np.ndarray   # [nlist, dim] f32
+    codebooks: np.ndarray   # [pq_m, ks, dsub] f32
+    codes: np.ndarray       # [n, pq_m] u8 by id
+    dataset: np.ndarray     # [n, dim] f32
+    assign: np.ndarray      # [n] i32
+    lists: list             # nlist arrays of i64 ids
+
+    def packed(self):
+        """List-major (packed_codes [n, pq_m], packed_ids [n], offsets [nlist+1])."""
+        ids = np.concatenate([np.asarray(l, dtype=np.int64) for l in self.lists]) \
+            if self.n else np.zeros(0, np.int64)
+        offsets = np.zeros(self.nlist + 1, dtype=np.int64)
+        offsets[1:] = np.cumsum([len(l) for l in self.lists])
+        return np.ascontiguousarray(self.codes[ids]), ids, offsets
+
+
+def read_ipq1(path) -> Ipq1:
+    raw = Path(path).read_bytes()
+    head = np.frombuffer(raw, dtype=np.uint8, count=44)
+    magic, version = np.frombuffer(head[:8].tobytes(), dtype=np.int32)
+    if np.uint32(magic) != 0x31515049 or version != 1:
+        raise ValueError("not an IPQ1 v1 file")
+    n, dim = (int(v) for v in np.frombuffer(head[8:24].tobytes(), dtype=np.int64))
+    nlist, pq_m, pq_ks, dsub, metric = (int(v) for v in np.frombuffer(head[24:44].tobytes(),
+                                                                       dtype=np.int32))
+    off = 44
+
+    def take(dtype, count):
+        nonlocal off
+        a = np.frombuffer(raw, dtype=dtype, count=count, offset=off)
+        off += a.nbytes
+        return a.copy()
+
+    centroids = take(np.float32, nlist * dim).reshape(nlist, dim)
+    codebooks = take(np.float32, pq_m * pq_ks * dsub).reshape(pq_m, pq_ks, dsub)
+    codes = take(np.uint8, n * pq_m).reshape(n, pq_m)
+    dataset = take(np.float32, n * dim).reshape(n, dim)
+    assign = take(np.int32, n)
+    lists = []
+    for _ in range(nlist):
+        size = int(take(np.int32, 1)[0])
+        lists.append(take(np.int64, size))
+    if off != len(raw):
+        raise ValueError("trailing bytes in IPQ1 file")
+    return Ipq1(n, dim, nlist, pq_m, pq_ks, dsub, metric, centroids, codebooks, codes, dataset,
+                assign, lists)
+
+
+class _OracleIndex(ctypes.Structure):
+    _fields_ = [
+        ("n", c_int64), ("dim", c_int64), ("nlist", c_int32), ("pq_m", c_int32),
+        ("pq_ks", c_int32), ("dsub", c_int32), ("metric", c_int32), ("pad_", c_int32),
+        ("centroids", POINTER(c_float)), ("codebooks", POINTER(c_float)),
+        ("packed_codes", POINTER(c_uint8)), ("packed_ids", POINTER(c_int64)),
+        ("list_offsets", POINTER(c_int64)), ("dataset", POINTER(c_float)),
+    ]
+
+
+def _f32p(a):
+    return a.ctypes.data_as(POINTER(c_float))
+
+
+def _i64p(a):
+    return a.ctypes.data_as(POINTER(c_int64))
+
+
+class Oracle:
+    """ctypes front end of oracle/liboracle.so over one IPQ1 index."""
+
+    def __init__(self, ix: Ipq1):
+        self.lib = ctypes.CDLL(str(ORACLE_SO))
+        L = self.lib
+        L.oracle_ivfpq_search.restype = c_int32
+        L.oracle_ivfpq_search.argtypes = [POINTER(_OracleIndex), POINTER(c_float), c_int64,
+                                          c_int64, c_int32, c_int32, c_void_p, c_int32,
+                                          POINTER(c_int64), POINTER(c_float)]
+        L.oracle_probe.restype = c_int32
+        L.oracle_probe.argtypes = [POINTER(_OracleIndex), POINTER(c_float), c_int64, c_int32,
+                                   POINTER(c_int64)]
+        L.oracle_shortlist.restype = c_int64
+        L.oracle_shortlist.argtypes = [POINTER(_OracleIndex), POINTER(c_float), POINTER(c_int64),
+                                       c_int32, c_int32, c_void_p, c_int32, POINTER(c_int64),
+                                       POINTER(c_float), POINTER(c_int64)]
+        L.oracle_lut.restype = None
+        L.oracle_lut.argtypes = [POINTER(_OracleIndex), POINTER(c_float), c_int32, c_int32,
+                                 POINTER(c_float)]
+        self.ix = ix
+        codes, ids, offsets = ix.packed()
+        self._keep = [np.ascontiguousarray(ix.centroids), np.ascontiguousarray(ix.codebooks),
+                      codes, ids, offsets, np.ascontiguousarray(ix.dataset)]
+        c, cb, pc, pi, po, ds = self._keep
+        self.packed_ids = ids
+        self.offsets = offsets
+        self.s = _OracleIndex(ix.n, ix.dim, ix.nlist, ix.pq_m, ix.pq_ks, ix.dsub, ix.metric, 0,
+                              _f32p(c), _f32p(cb), pc.ctypes.data_as(POINTER(c_uint8)), _i64p(pi),
+                              _i64p(po), _f32p(ds))
+
+    def search(self, queries, k, nprobe, krefine, bitset=None, lut_f16=False):
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.ix.dim)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), dtype=np.int64)
+        dists = np.empty((nq, k), dtype=np.float32)
+        b = None if bitset is None else np.ascontiguousarray(bitset, dtype=np.uint8)
+        rc = self.lib.oracle_ivfpq_search(ctypes.byref(self.s), _f32p(q), nq, k, nprobe, krefine,
+                                          None if b is None else b.ctypes.data_as(c_void_p),
+                                          int(bool(lut_f16)), _i64p(ids), _f32p(dists))
+        if rc != 0:
+            raise MemoryError("oracle search failed")
+        return ids, dists
+
+    def probes(self, queries, nprobe):
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.ix.dim)
+        P = max(1, min(int(nprobe), self.ix.nlist))
+        out = np.empty((q.shape[0], P), dtype=np.int64)
+        if self.lib.oracle_probe(ctypes.byref(self.s), _f32p(q), q.shape[0], P, _i64p(out)) != 0:
+            raise MemoryError("oracle probe failed")
+        return out
+
+    def shortlist(self, query, probes, R, bitset=None, lut_f16=False):
+        q = np.ascontiguousarray(query, dtype=np.float32).reshape(self.ix.dim)
+        p = np.ascontiguousarray(probes, dtype=np.int64)
+        pos = np.empty(int(R), dtype=np.int64)
+        sc = np.empty(int(R), dtype=np.float32)
+        total = c_int64()
+        b = None if bitset is None else np.ascontiguousarray(bitset, dtype=np.uint8)
+        kr = self.lib.oracle_shortlist(ctypes.byref(self.s), _f32p(q), _i64p(p), p.size, int(R),
+                                       None if b is None else b.ctypes.data_as(c_void_p),
+                                       int(bool(lut_f16)), _i64p(pos), _f32p(sc),
+                                       ctypes.byref(total))
+        return pos[:kr], sc[:kr], int(total.value)
+
+    def lut(self, query, list_id, lut_f16=False):
+        q = np.ascontiguousarray(query, dtype=np.float32).reshape(self.ix.dim)
+        t = np.empty((self.ix.pq_m, self.ix.pq_ks), dtype=np.float32)
+        self.lib.oracle_lut(ctypes.byref(self.s), _f32p(q), int(list_id), int(bool(lut_f16)),
+                            _f32p(t))
+        return t
+
+
+def oracle_lib():
+    lib = ctypes.CDLL(str(ORACLE_SO))
+    lib.oracle_f32_to_f16.restype = c_uint16
+    lib.oracle_f32_to_f16.argtypes = [c_float]
+    lib.oracle_f16_to_f32.restype = c_float
+    lib.oracle_f16_to_f32.argtypes = [c_uint16]
+    lib.oracle_topk.restype = c_int64
+    lib.oracle_topk.argtypes = [POINTER(c_float), c_int64, c_int64, POINTER(c_int64),
+                                POINTER(c_float)]
+    lib.oracle_brute_force.restype = c_int32
+    lib.oracle_brute_force.argtypes = [POINTER(c_float), c_int64, c_int64, c_int32,
+                                       POINTER(c_float), c_int64, c_int64, POINTER(c_int64),
+                                       POINTER(c_float)]
+    lib.oracle_refine_distance.restype = c_float
+    lib.oracle_refine_distance.argtypes = [c_int32, POINTER(c_float), POINTER(c_float), c_int64]
+    return lib
+
+
+def brute_force(dataset, queries, k, metric=0):
+    lib = oracle_lib()
+    x = np.ascontiguousarray(dataset, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    ids = np.empty((q.shape[0], k), dtype=np.int64)
+    d = np.empty((q.shape[0], k), dtype=np.float32)
+    lib.oracle_brute_force(_f32p(x), x.shape[0], x.shape[1], metric, _f32p(q), q.shape[0], k,
+                           _i64p(ids), _f32p(d))
+    return ids, d
+
+
+class Reference:
+    """The reference libovvs (built from /root/reference into oracle/_ref), CPU route."""
+
+    def __init__(self):
+        if not REF_SO.exists():
+            raise FileNotFoundError(f"{REF_SO} is not built (make -C oracle ref)")
+        L = ctypes.CDLL(str(REF_SO))
+        V = c_void_p
+        sigs = {
+            "ovvsResourcesCreate": [POINTER(V)],
+            "ovvsResourcesDestroy": [V],
+            "ovvsResourcesSetPolicy": [V, c_int32],
+            "ovvsIvfPqBuild": [V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32, c_int32,
+                               c_int32, POINTER(V)],
+            "ovvsIvfPqSearch": [V, V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32, V,
+                                POINTER(c_int64), POINTER(c_float)],
+            "ovvsIvfPqSerialize": [V, c_char_p],
+            "ovvsIvfPqDeserialize": [V, c_char_p, POINTER(V)],
+            "ovvsIvfPqExtend": [V, V, POINTER(c_float), c_int64],
+            "ovvsIvfPqDestroy": [V],
+        }
+        for name, args in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = c_int32
+            fn.argtypes = args
+        self.lib = L
+        self.res = c_void_p()
+        assert L.ovvsResourcesCreate(ctypes.byref(self.res)) == 0
+        assert L.ovvsResourcesSetPolicy(self.res, FORCE_CPU) == 0
+
+    def close(self):
+        if self.res:
+            self.lib.ovvsResourcesDestroy(self.res)
+            self.res = None
+
+    def build(self, data, metric, nlist, pq_m, nbits):
+        x = np.ascontiguousarray(data, dtype=np.float32)
+        h = c_void_p()
+        rc = self.lib.ovvsIvfPqBuild(self.res, _f32p(x), x.shape[0], x.shape[1], metric, nlist,
+                                     pq_m, nbits, ctypes.byref(h))
+        return rc, h
+
+    def load(self, path):
+        h = c_void_p()
+        rc = self.lib.ovvsIvfPqDeserialize(self.res, str(path).encode(), ctypes.byref(h))
+        return rc, h
+
+    def save(self, h, path):
+        return self.lib.ovvsIvfPqSerialize(h, str(path).encode())
+
+    def extend(self, h, extra):
+        x = np.ascontiguousarray(extra, dtype=np.float32)
+        return self.lib.ovvsIvfPqExtend(self.res, h, _f32p(x), x.shape[0])
+
+    def search(self, h, queries, k, nprobe, krefine, bitset=None):
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        nq = q.shape[0]
+        ids = np.full((nq, k), -9, dtype=np.int64)
+        d = np.full((nq, k), -9.0, dtype=np.float32)
+        b = None if bitset is None else np.ascontiguousarray(bitset, dtype=np.uint8)
+        rc = self.lib.ovvsIvfPqSearch(self.res, h, _f32p(q), nq, k, nprobe, krefine,
+                                      None if b is None else b.ctypes.data_as(c_void_p),
+                                      _i64p(ids), _f32p(d))
+        return rc, ids, d
+
+    def destroy(self, h):
+        if h:
+            self.lib.ovvsIvfPqDestroy(h)

@@ -1,0 +1,339 @@
+// ivf_pq_search.cpp — ovvsIvfPqSearch and its additive variants on one MI355X.
+//
+// Reference: ovvsIvfPqSearch, src/neighbors/indexes.cpp:538-1134. The argument
+// checks, their order and their status codes follow the reference (:541-575);
+// the clamps are nprobe := clamp(nprobe, 1, nlist) and krefine := max(krefine,
+// k); outputs are staged and published only on success (:1101-1102); telemetry
+// is merged only on success (:1103-1125).
+//
+// Device pipeline per call, all on the Resources stream:
+//   1. query norms                          ovvs_hip_row_norms
+//   2. coarse scores, chunked over queries  ovvs_hip_coarse_scores
+//   3. probe selection                      ovvs_hip_select_topk
+//   4. fused LUT + code scan + shortlist    ovvs_hip_scan
+//   5. exact re-rank + final select         ovvs_hip_refine
+// There is no host compute path: without a usable GPU the call fails with
+// OVVS_STATUS_DEVICE_UNAVAILABLE.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <limits>
+#include <new>
+
+#include "internal.hpp"
+
+using ovvs::GpuWork;
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Budget for one chunk of the [queries x nlist] coarse score matrix.
+constexpr size_t kScoreChunkBytes = size_t(512) << 20;
+
+int64_t elapsed_ns(Clock::time_point a, Clock::time_point b) {
+  const auto d = std::chrono::duration_cast<std::chrono::nanoseconds>(b - a).count();
+  return d > 0 ? d : 0;
+}
+
+int64_t event_ns(hipEvent_t a, hipEvent_t b) {
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, a, b) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return static_cast<int64_t>(static_cast<double>(ms) * 1e6);
+}
+
+struct Carver {
+  unsigned char* base;
+  size_t off = 0;
+  template <class T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base + off);
+    off += align256(count * sizeof(T));
+    return p;
+  }
+};
+
+#define SEARCH_HIP(expr)                            \
+  do {                                              \
+    const hipError_t hip_e_ = (expr);               \
+    if (hip_e_ != hipSuccess) {                     \
+      (void)hipGetLastError();                      \
+      return ovvs::status_from_hip(hip_e_);         \
+    }                                               \
+  } while (0)
+
+#define SEARCH_TRY(expr)                      \
+  do {                                        \
+    const ovvsStatus st_ = (expr);            \
+    if (st_ != OVVS_STATUS_SUCCESS) return st_; \
+  } while (0)
+
+ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float* queries,
+                       int64_t nq, int64_t k, int32_t nprobe, int32_t krefine,
+                       const uint8_t* bitset, ovvsDType lut_dtype, bool device_io,
+                       int64_t* neighbors, float* distances) {
+  const auto started = Clock::now();
+  if (!res || !index || !queries || !neighbors || !distances || nq <= 0 || k <= 0 ||
+      k > std::numeric_limits<int32_t>::max()) {
+    return OVVS_STATUS_INVALID_ARGUMENT;
+  }
+  if (nq > std::numeric_limits<int64_t>::max() / k ||
+      static_cast<uint64_t>(nq) >
+          static_cast<uint64_t>(std::numeric_limits<size_t>::max() / sizeof(int64_t)) /
+              static_cast<uint64_t>(k)) {
+    return OVVS_STATUS_SHAPE_MISMATCH;
+  }
+  ovvsIvfPqIndexImpl& ix = *index;
+  if (ix.n <= 0 || ix.dim <= 0 || ix.nlist <= 0 || ix.pq_m <= 0 || ix.pq_ks <= 0 ||
+      ix.lists.size() != static_cast<size_t>(ix.nlist) ||
+      ix.codes.size() != static_cast<size_t>(ix.n) * static_cast<size_t>(ix.pq_m) ||
+      static_cast<uint64_t>(nq) >
+          static_cast<uint64_t>(std::numeric_limits<size_t>::max() / sizeof(float)) /
+              static_cast<uint64_t>(ix.dim) ||
+      static_cast<uint64_t>(nq) >
+          static_cast<uint64_t>(std::numeric_limits<size_t>::max() / sizeof(int64_t)) /
+              static_cast<uint64_t>(ix.nlist)) {
+    return OVVS_STATUS_INVALID_ARGUMENT;
+  }
+  if (lut_dtype != OVVS_DTYPE_F32 && lut_dtype != OVVS_DTYPE_F16) return OVVS_STATUS_UNSUPPORTED;
+  const int32_t P = std::max(1, std::min(nprobe, ix.nlist));
+  const int32_t R = krefine < static_cast<int32_t>(k) ? static_cast<int32_t>(k) : krefine;
+  const int lut_f16 = lut_dtype == OVVS_DTYPE_F16 ? 1 : 0;
+  // Fixed limits of the kernels: fail closed, as the reference's GPU route does
+  // for krefine > 128 (indexes.cpp:576-584).
+  if (R > OVVS_HIP_MAX_REFINE || P > OVVS_HIP_MAX_PROBES ||
+      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16) == 0 ||
+      nq > 0x7fffffff) {
+    return OVVS_STATUS_DEVICE_UNAVAILABLE;
+  }
+
+  try {
+    std::lock_guard<std::mutex> lock(res->call_mutex);
+    SEARCH_TRY(res->ensure_gpu());
+    GpuWork work;
+    SEARCH_TRY(ix.ensure_device(*res, work));
+    const ovvs::IndexDevice& dv = *ix.dev;
+    hipStream_t s = res->stream;
+    const int32_t dim = static_cast<int32_t>(ix.dim);
+
+    // Query chunk for the coarse score matrix.
+    int64_t qc = static_cast<int64_t>(kScoreChunkBytes / (static_cast<size_t>(ix.nlist) * 4));
+    qc = std::max<int64_t>(1, std::min<int64_t>(qc, nq));
+    const size_t nqk = static_cast<size_t>(nq) * static_cast<size_t>(k);
+    const size_t bitset_bytes = static_cast<size_t>((ix.n + 7) / 8);
+
+    size_t need = 0;
+    need += device_io ? 0 : align256(static_cast<size_t>(nq) * dim * 4);  // queries
+    need += align256(static_cast<size_t>(nq) * 4);                        // query norms
+    need += align256(static_cast<size_t>(nq) * P * 4);                    // probes
+    need += align256(static_cast<size_t>(qc) * ix.nlist * 4);             // score chunk
+    need += align256(static_cast<size_t>(nq) * R * 8);                    // shortlist keys
+    need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
+    need += align256(static_cast<size_t>(nq) * 4);                        // shortlist counts
+    need += align256(nqk * 8) + align256(nqk * 4);                        // staged outputs
+    need += align256(4 * 8);                                              // counters
+    need += (!device_io && bitset) ? align256(bitset_bytes) : 0;
+    SEARCH_TRY(res->reserve_workspace(need, work));
+    const size_t pinned_need = 4 * 8 + (device_io ? 0 : nqk * 12);
+    SEARCH_TRY(res->reserve_pinned(pinned_need));
+
+    Carver cv{static_cast<unsigned char*>(res->workspace.get())};
+    const float* d_q = device_io ? queries : nullptr;
+    if (!device_io) d_q = cv.take<float>(static_cast<size_t>(nq) * dim);
+    float* d_qn = cv.take<float>(static_cast<size_t>(nq));
+    int32_t* d_probes = cv.take<int32_t>(static_cast<size_t>(nq) * P);
+    float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
+    uint64_t* d_skeys = cv.take<uint64_t>(static_cast<size_t>(nq) * R);
+    int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
+    int32_t* d_scnt = cv.take<int32_t>(static_cast<size_t>(nq));
+    int64_t* d_oid = cv.take<int64_t>(nqk);
+    float* d_odist = cv.take<float>(nqk);
+    unsigned long long* d_counters = cv.take<unsigned long long>(4);
+    const uint8_t* d_bitset = device_io ? bitset : nullptr;
+    if (!device_io && bitset) {
+      uint8_t* b = cv.take<uint8_t>(bitset_bytes);
+      SEARCH_HIP(hipMemcpyAsync(b, bitset, bitset_bytes, hipMemcpyHostToDevice, s));
+      ovvs::saturating_add(work.h2d_calls, 1);
+      ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(bitset_bytes));
+      d_bitset = b;
+    }
+    if (!device_io) {
+      const size_t qb = static_cast<size_t>(nq) * dim * 4;
+      SEARCH_HIP(hipMemcpyAsync(const_cast<float*>(d_q), queries, qb, hipMemcpyHostToDevice, s));
+      ovvs::saturating_add(work.h2d_calls, 1);
+      ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(qb));
+    }
+    SEARCH_HIP(hipMemsetAsync(d_counters, 0, 4 * 8, s));
+
+    hipEvent_t* ev = res->events;
+    SEARCH_HIP(hipEventRecord(ev[0], s));
+    SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
+    int64_t chunks = 0;
+    for (int64_t q0 = 0; q0 < nq; q0 += qc) {
+      const int64_t cnt = std::min(qc, nq - q0);
+      SEARCH_HIP(ovvs_hip_coarse_scores(d_q + q0 * dim, d_qn + q0, cnt, dv.centroids.as<float>(),
+                                        dv.cnorm.as<float>(), ix.nlist, dim, d_scores, ix.nlist,
+                                        s));
+      if (q0 == 0) SEARCH_HIP(hipEventRecord(ev[1], s));
+      SEARCH_HIP(ovvs_hip_select_topk(d_scores, ix.nlist, cnt, ix.nlist, P, d_probes + q0 * P, s));
+      ++chunks;
+    }
+    SEARCH_HIP(hipEventRecord(ev[2], s));
+
+    OvvsScanArgs sa{};
+    sa.queries = d_q;
+    sa.nq = nq;
+    sa.dim = dim;
+    sa.P = P;
+    sa.probes = d_probes;
+    sa.centroids = dv.centroids.as<float>();
+    sa.codebooks = dv.codebooks.as<float>();
+    sa.pq_m = ix.pq_m;
+    sa.ks = ix.pq_ks;
+    sa.dsub = ix.dsub;
+    sa.code_stride = dv.code_stride;
+    sa.list_offsets = dv.offsets.as<int64_t>();
+    sa.codes = dv.codes.as<uint8_t>();
+    sa.ids = dv.ids.as<int64_t>();
+    sa.bitset = d_bitset;
+    sa.K = R;
+    sa.lut_f16 = lut_f16;
+    sa.out_keys = d_skeys;
+    sa.out_pos = d_spos;
+    sa.out_count = d_scnt;
+    sa.counters = d_counters;
+    SEARCH_HIP(ovvs_hip_scan(&sa, s));
+    SEARCH_HIP(hipEventRecord(ev[3], s));
+
+    OvvsRefineArgs ra{};
+    ra.queries = d_q;
+    ra.qnorm = d_qn;
+    ra.nq = nq;
+    ra.dim = dim;
+    ra.metric = static_cast<int32_t>(ix.metric);
+    ra.dataset = dv.dataset.as<float>();
+    ra.xnorm = dv.xnorm.as<float>();
+    ra.ids = dv.ids.as<int64_t>();
+    ra.K = R;
+    ra.short_pos = d_spos;
+    ra.short_count = d_scnt;
+    ra.k = k;
+    ra.out_ids = d_oid;
+    ra.out_dist = d_odist;
+    SEARCH_HIP(ovvs_hip_refine(&ra, s));
+    SEARCH_HIP(hipEventRecord(ev[4], s));
+    work.kernel_launches += 3 + 2 * chunks;
+
+    unsigned char* pin = static_cast<unsigned char*>(res->pinned);
+    SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));
+    ovvs::saturating_add(work.d2h_calls, 1);
+    ovvs::saturating_add(work.d2h_bytes, 32);
+    if (!device_io) {
+      SEARCH_HIP(hipMemcpyAsync(pin + 32, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
+      SEARCH_HIP(hipMemcpyAsync(pin + 32 + nqk * 8, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));
+      ovvs::saturating_add(work.d2h_calls, 2);
+      ovvs::saturating_add(work.d2h_bytes, static_cast<int64_t>(nqk * 12));
+    }
+    ovvs::saturating_add(work.wait_calls, 1);
+    SEARCH_HIP(hipStreamSynchronize(s));
+
+    // Success: publish the outputs.
+    if (device_io) {
+      SEARCH_HIP(hipMemcpyAsync(neighbors, d_oid, nqk * 8, hipMemcpyDeviceToDevice, s));
+      SEARCH_HIP(hipMemcpyAsync(distances, d_odist, nqk * 4, hipMemcpyDeviceToDevice, s));
+      ovvs::saturating_add(work.wait_calls, 1);
+      SEARCH_HIP(hipStreamSynchronize(s));
+    } else {
+      std::memcpy(neighbors, pin + 32, nqk * 8);
+      std::memcpy(distances, pin + 32 + nqk * 8, nqk * 4);
+    }
+
+    unsigned long long counters[4];
+    std::memcpy(counters, pin, sizeof(counters));
+    ovvsIvfPqSearchStatsV1 d{};
+    d.successful_calls = 1;
+    d.blocks = chunks;
+    d.queries = nq;
+    d.tasks = static_cast<int64_t>(std::min<unsigned long long>(counters[1], INT64_MAX));
+    d.candidate_rows = static_cast<int64_t>(std::min<unsigned long long>(counters[0], INT64_MAX));
+    d.selected_rows = static_cast<int64_t>(std::min<unsigned long long>(counters[2], INT64_MAX));
+    if (chunks == 1) {
+      d.coarse_pairwise_ns = event_ns(ev[0], ev[1]);
+      d.coarse_topk_ns = event_ns(ev[1], ev[2]);
+    } else {
+      d.coarse_pairwise_ns = event_ns(ev[0], ev[2]);
+    }
+    d.adc_scan_select_ns = event_ns(ev[2], ev[3]);
+    d.refine_distance_ns = event_ns(ev[3], ev[4]);
+    d.total_wall_ns = elapsed_ns(started, Clock::now());
+    int64_t named = 0;
+    ovvs::saturating_add(named, d.coarse_pairwise_ns);
+    ovvs::saturating_add(named, d.coarse_topk_ns);
+    ovvs::saturating_add(named, d.adc_scan_select_ns);
+    ovvs::saturating_add(named, d.refine_distance_ns);
+    d.planning_ns = d.total_wall_ns > named ? d.total_wall_ns - named : 0;
+    d.gpu_allocation_calls = work.allocation_calls;
+    d.gpu_allocation_bytes = work.allocation_bytes;
+    d.gpu_h2d_calls = work.h2d_calls;
+    d.gpu_h2d_bytes = work.h2d_bytes;
+    d.gpu_d2h_calls = work.d2h_calls;
+    d.gpu_d2h_bytes = work.d2h_bytes;
+    d.gpu_kernel_launches = work.kernel_launches;
+    d.gpu_wait_calls = work.wait_calls;
+    {
+      std::lock_guard<std::mutex> stats_lock(res->stats_mutex);
+      ovvsIvfPqSearchStatsV1& t = res->stats;
+      t.abi_version = OVVS_IVF_PQ_SEARCH_STATS_ABI_V1;
+      t.struct_size = sizeof(t);
+      int64_t* dst = &t.successful_calls;
+      const int64_t* src = &d.successful_calls;
+      for (int i = 0; i < 24; ++i) ovvs::saturating_add(dst[i], src[i]);
+    }
+    res->last_device = OVVS_DEVICE_GPU;
+    res->last_compute_dtype = lut_f16 ? OVVS_DTYPE_F16 : OVVS_DTYPE_F32;
+    return OVVS_STATUS_SUCCESS;
+  } catch (const std::bad_alloc&) {
+    return OVVS_STATUS_OOM;
+  } catch (...) {
+    return OVVS_STATUS_ERROR;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+OVVS_API ovvsStatus ovvsIvfPqSearch(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                    const float* queries, int64_t nq, int64_t k, int32_t nprobe,
+                                    int32_t krefine, const uint8_t* bitset, int64_t* neighbors,
+                                    float* distances) {
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, OVVS_DTYPE_F32, false,
+                     neighbors, distances);
+}
+
+OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                      const float* queries, int64_t nq, int64_t k,
+                                      int32_t nprobe, int32_t krefine, const uint8_t* bitset,
+                                      ovvsDType lut_dtype, int64_t* neighbors,
+                                      float* distances) {
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, false,
+                     neighbors, distances);
+}
+
+OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                          const float* queries, int64_t nq, int64_t k,
+                                          int32_t nprobe, int32_t krefine,
+                                          const uint8_t* bitset, ovvsDType lut_dtype,
+                                          int64_t* neighbors, float* distances) {
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, true,
+                     neighbors, distances);
+}
+
+}  // extern "C"

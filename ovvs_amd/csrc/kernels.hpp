@@ -1,0 +1,128 @@
+// kernels.hpp — the thin C ABI between libovvs's C++ host code and its gfx950
+// HIP kernels. Every function enqueues work on `stream` and returns the launch
+// status (hipSuccess == 0); none of them synchronizes or allocates. Shapes are
+// validated by the host caller before launch; each launcher re-checks the
+// limits its kernel relies on and returns hipErrorInvalidValue instead of
+// launching when they do not hold.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Largest shortlist (krefine) and final k the scan/refine kernels hold in
+// registers: 64 keys per lane-row, up to 4 rows per wave.
+#define OVVS_HIP_MAX_REFINE 256
+// Largest probe count the in-LDS probe selection sorts (32 KiB of 64-bit keys).
+#define OVVS_HIP_MAX_PROBES 4096
+
+// out[i] = sum_t x[i*dim+t]^2, left to right from +0 (reference internal.hpp:221-225).
+hipError_t ovvs_hip_row_norms(const float* x, int64_t n, int32_t dim, float* out,
+                              hipStream_t stream);
+
+// Exact expanded-L2 coarse scores: S[q*ldS + c] = (qn[q] + cn[c]) - 2*dot(q, c),
+// dot a left-to-right fp32 sum (reference mixer.cpp:177-198, cpu_prims.cpp:48-58).
+hipError_t ovvs_hip_coarse_scores(const float* Q, const float* qn, int64_t nq, const float* C,
+                                  const float* cn, int32_t nlist, int32_t dim, float* S,
+                                  int64_t ldS, hipStream_t stream);
+
+// Per row, the first P columns of S under the total order (score ascending,
+// +-0 equal, NaN last, column ascending), written in rank order to
+// out[row*P + r] (reference cpu_prims.cpp:24-106). P <= OVVS_HIP_MAX_PROBES, P <= N.
+hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N, int32_t P,
+                                int32_t* out, hipStream_t stream);
+
+// Exact argmin over all centroids for each row of Q (top-1 of the coarse score
+// under the same total order), fused with the score computation: labels[i].
+hipError_t ovvs_hip_coarse_argmin(const float* Q, const float* qn, int64_t nq, const float* C,
+                                  const float* cn, int32_t nlist, int32_t dim, int32_t* labels,
+                                  hipStream_t stream);
+
+struct OvvsScanArgs {
+  const float* queries;        // [nq * dim]
+  int64_t nq;
+  int32_t dim;
+  int32_t P;                   // probes per query
+  const int32_t* probes;       // [nq * P] list ids in rank order
+  const float* centroids;      // [nlist * dim]
+  const float* codebooks;      // [pq_m * ks * dsub]
+  int32_t pq_m;
+  int32_t ks;                  // power of two, 16..256
+  int32_t dsub;
+  int32_t code_stride;         // bytes per packed row, multiple of 16
+  const int64_t* list_offsets; // [nlist + 1]
+  const uint8_t* codes;        // [n * code_stride], list-major
+  const int64_t* ids;          // [n], list-major
+  const uint8_t* bitset;       // (n+7)/8 bytes or nullptr
+  int32_t K;                   // shortlist length (krefine), 1..OVVS_HIP_MAX_REFINE
+  int32_t lut_f16;             // 0: fp32 table entries, 1: binary16 entries
+  uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
+  int32_t* out_pos;            // [nq * K] packed positions
+  int32_t* out_count;          // [nq]
+  unsigned long long* counters; // [3]: += scanned rows, += non-empty (query, list) tasks,
+                                //      += shortlist entries
+};
+
+// Fused residual-LUT build (in LDS) + ADC code scan + per-query shortlist of
+// the K best (ADC score, dense ordinal) rows over all probed lists.
+hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
+// Dynamic LDS bytes the scan kernel needs for these shapes (0 if unsupported).
+size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16);
+
+struct OvvsRefineArgs {
+  const float* queries;   // [nq * dim]
+  const float* qnorm;     // [nq]
+  int64_t nq;
+  int32_t dim;
+  int32_t metric;         // ovvsMetric
+  const float* dataset;   // [n * dim], row = id
+  const float* xnorm;     // [n]
+  const int64_t* ids;     // [n] list-major (packed position -> id)
+  int32_t K;              // shortlist stride
+  const int32_t* short_pos;    // [nq * K]
+  const int32_t* short_count;  // [nq]
+  int64_t k;              // outputs per query
+  int64_t* out_ids;       // [nq * k]
+  float* out_dist;        // [nq * k]
+};
+
+// Exact re-rank of each query's shortlist by the index metric and final select
+// of the first min(k, count) by (distance, shortlist rank); (-1, +inf) padding;
+// inner-product distances are returned as +ip (reference indexes.cpp:1067-1096).
+hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream);
+
+// ---- index build helpers (reference indexes.cpp:459-536, mixer.cpp:866-921) ----
+
+// out[i*dsub+u] = x[i*dim + m*dsub + u]
+hipError_t ovvs_hip_gather_sub(const float* x, int64_t n, int32_t dim, int32_t m, int32_t dsub,
+                               float* out, hipStream_t stream);
+// out[i*dim+t] = x[i*dim+t] - C[labels[i]*dim+t]
+hipError_t ovvs_hip_residuals(const float* x, int64_t n, int32_t dim, const int32_t* labels,
+                              const float* C, float* out, hipStream_t stream);
+// out[c*dim+t] = x[rows[c]*dim+t]
+hipError_t ovvs_hip_gather_rows(const float* x, int32_t dim, const int64_t* rows, int32_t count,
+                                float* out, hipStream_t stream);
+// Stable grouping of rows by label: order[] lists row indices grouped by label,
+// ascending within a label; offsets[c] = first slot of label c, offsets[k] = n.
+// temp/temp_bytes: scratch from ovvs_hip_group_temp_bytes.
+size_t ovvs_hip_group_temp_bytes(int64_t n);
+hipError_t ovvs_hip_group_by_label(const int32_t* labels, int64_t n, int32_t k,
+                                   int32_t* sorted_labels, int32_t* order, int64_t* offsets,
+                                   void* temp, size_t temp_bytes, hipStream_t stream);
+// Lloyd mean update: for each centroid with rows, C[c] = (sum of its rows,
+// left to right in row order) * (1/count); empty centroids keep their value.
+hipError_t ovvs_hip_kmeans_update(const float* x, int32_t dim, const int32_t* order,
+                                  const int64_t* offsets, int32_t k, float* C,
+                                  hipStream_t stream);
+// codes[i*pq_m+m] = argmin_j l2(resid_i,m - B[m][j]), first minimum wins
+// (reference indexes.cpp:211-229).
+hipError_t ovvs_hip_pq_encode(const float* resid, int64_t n, int32_t dim, int32_t pq_m,
+                              int32_t ks, int32_t dsub, const float* codebooks, uint8_t* codes,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif

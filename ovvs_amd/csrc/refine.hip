@@ -1,0 +1,119 @@
+// refine.hip — exact re-rank of the IVF-PQ shortlist on gfx950.
+//
+// Reference behaviour (src/neighbors/indexes.cpp:1067-1096): gather the dataset
+// rows of the shortlisted ids, compute the index metric exactly
+// (src/prim/mixer.cpp:177-221 for the expanded metrics, src/internal.hpp:240-272
+// for the others), keep the first min(k, kr) under the total order on
+// (distance, shortlist rank), flip the sign back for inner product, and pad the
+// remaining slots with (-1, +inf).
+//
+// One wave64 per query: each lane scores shortlist entries i = lane, lane+64, ...
+// with left-to-right fp32 sums, the (key, rank) pairs are sorted in LDS by a
+// single-wave bitonic network, and the first k slots are written.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+using namespace ovvs_dev;
+
+namespace {
+
+enum { kL2 = 0, kL2Sqrt = 1, kIP = 2, kCosine = 3, kHamming = 4, kLp = 5 };
+
+// std::max semantics for floats: keeps `a` unless a < b.
+__device__ __forceinline__ float ref_max(float a, float b) { return (a < b) ? b : a; }
+
+__device__ float metric_value(int metric, const float* __restrict__ q,
+                              const float* __restrict__ x, int dim, float qn, float xn) {
+  switch (metric) {
+    case kL2:
+      return (qn + xn) - 2.f * seq_dot(q, x, dim);
+    case kIP:
+      return -seq_dot(q, x, dim);
+    case kCosine: {
+      const float ip = seq_dot(q, x, dim);
+      const float a = __fsqrt_rn(ref_max(qn, 1e-12f));
+      const float b = __fsqrt_rn(ref_max(xn, 1e-12f));
+      return 1.f - __fdiv_rn(ip, a * b);
+    }
+    case kL2Sqrt:
+      return __fsqrt_rn(seq_l2sq(q, x, dim));
+    case kHamming: {
+      int s = 0;
+      for (int i = 0; i < dim; ++i) s += static_cast<int>((q[i] >= 0.f) != (x[i] >= 0.f));
+      return static_cast<float>(s);
+    }
+    case kLp: {
+      // Minkowski p = 2 as the search passes it (reference indexes.cpp:1076).
+      float s = 0.f;
+      for (int i = 0; i < dim; ++i) s = s + powf(fabsf(q[i] - x[i]), 2.f);
+      return powf(s, 0.5f);
+    }
+    default:
+      return seq_l2sq(q, x, dim);
+  }
+}
+
+__global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a) {
+  __shared__ uint64_t keys[OVVS_HIP_MAX_REFINE];
+  __shared__ float vals[OVVS_HIP_MAX_REFINE];
+  const int64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* __restrict__ qv = a.queries + q * a.dim;
+  int cnt = a.short_count[q];
+  cnt = cnt < 0 ? 0 : (cnt > a.K ? a.K : cnt);
+  int M = 1;
+  while (M < cnt) M <<= 1;
+  for (int i = lane; i < M; i += 64) {
+    if (i < cnt) {
+      const int64_t id = a.ids[a.short_pos[q * a.K + i]];
+      const float v = metric_value(a.metric, qv, a.dataset + id * a.dim, a.dim, a.qnorm[q],
+                                   a.xnorm[id]);
+      keys[i] = make_key(v, static_cast<uint32_t>(i));
+      vals[i] = v;
+    } else {
+      keys[i] = kNoKey;
+    }
+  }
+  __syncthreads();
+  for (int k = 2; k <= M; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = lane; i < M; i += 64) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint64_t x = keys[i], y = keys[p];
+          if ((x > y) == ((i & k) == 0)) {
+            keys[i] = y;
+            keys[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int64_t kk = a.k < cnt ? a.k : cnt;
+  for (int64_t t = lane; t < a.k; t += 64) {
+    int64_t id = -1;
+    float d = __builtin_inff();
+    if (t < kk) {
+      const int i = static_cast<int>(keys[t] & 0xffffffffu);
+      id = a.ids[a.short_pos[q * a.K + i]];
+      d = a.metric == kIP ? -vals[i] : vals[i];
+    }
+    a.out_ids[q * a.k + t] = id;
+    a.out_dist[q * a.k + t] = d;
+  }
+}
+
+}  // namespace
+
+extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream) {
+  if (!args) return hipErrorInvalidValue;
+  const OvvsRefineArgs& a = *args;
+  if (a.nq <= 0) return hipSuccess;
+  if (!a.queries || !a.qnorm || !a.dataset || !a.xnorm || !a.ids || !a.short_pos ||
+      !a.short_count || !a.out_ids || !a.out_dist || a.dim <= 0 || a.K <= 0 ||
+      a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq)), dim3(64), 0, stream, a);
+  return hipGetLastError();
+}

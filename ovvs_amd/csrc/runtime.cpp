@@ -1,0 +1,266 @@
+// runtime.cpp — Resources, status strings, version, bitset helper and the
+// device-memory plumbing shared by the IVF-PQ entry points.
+//
+// Reference counterparts: src/rt/resources.cpp:14-147,218-229 and
+// src/rt/status.cpp:1-29. The reference's Resources carries SYCL queues, NPU
+// state, probe tables and CAGRA counters; this one carries what the IVF-PQ path
+// on one MI355X needs: a HIP stream, a grow-only device workspace, pinned host
+// staging, timing events and the IVF-PQ telemetry.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <new>
+
+#include "internal.hpp"
+
+namespace ovvs {
+
+hipError_t DeviceBuffer::allocate(size_t bytes) {
+  reset();
+  if (bytes == 0) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  ptr_ = p;
+  bytes_ = bytes;
+  return hipSuccess;
+}
+
+void DeviceBuffer::reset() {
+  if (ptr_) (void)hipFree(ptr_);
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
+void saturating_add(int64_t& value, int64_t delta) noexcept {
+  if (delta <= 0) return;
+  if (value > std::numeric_limits<int64_t>::max() - delta) {
+    value = std::numeric_limits<int64_t>::max();
+  } else {
+    value += delta;
+  }
+}
+
+bool gpu_present() {
+  static const bool present = [] {
+    int count = 0;
+    return hipGetDeviceCount(&count) == hipSuccess && count > 0;
+  }();
+  return present;
+}
+
+ovvsStatus status_from_hip(hipError_t e) {
+  switch (e) {
+    case hipSuccess:
+      return OVVS_STATUS_SUCCESS;
+    case hipErrorOutOfMemory:
+      return OVVS_STATUS_OOM;
+    case hipErrorNoDevice:
+    case hipErrorInvalidDevice:
+      return OVVS_STATUS_DEVICE_UNAVAILABLE;
+    default:
+      return OVVS_STATUS_ERROR;
+  }
+}
+
+}  // namespace ovvs
+
+ovvsResourcesImpl::~ovvsResourcesImpl() {
+  if (gpu_ready) {
+    (void)hipStreamSynchronize(stream);
+    for (hipEvent_t& e : events) {
+      if (e) (void)hipEventDestroy(e);
+    }
+    workspace.reset();
+    if (pinned) (void)hipHostFree(pinned);
+    (void)hipStreamDestroy(stream);
+  }
+}
+
+ovvsStatus ovvsResourcesImpl::ensure_gpu() {
+  if (policy == OVVS_POLICY_FORCE_CPU || policy == OVVS_POLICY_FORCE_NPU) {
+    return OVVS_STATUS_DEVICE_UNAVAILABLE;
+  }
+  if (gpu_ready) return OVVS_STATUS_SUCCESS;
+  if (!ovvs::gpu_present()) return OVVS_STATUS_DEVICE_UNAVAILABLE;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return OVVS_STATUS_DEVICE_UNAVAILABLE;
+  hipStream_t s = nullptr;
+  // Default stream priority, non-blocking with respect to the null stream.
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+    return OVVS_STATUS_DEVICE_UNAVAILABLE;
+  }
+  hipEvent_t ev[kEvents] = {};
+  for (int i = 0; i < kEvents; ++i) {
+    if (hipEventCreate(&ev[i]) != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      (void)hipStreamDestroy(s);
+      return OVVS_STATUS_DEVICE_UNAVAILABLE;
+    }
+  }
+  device = dev;
+  stream = s;
+  for (int i = 0; i < kEvents; ++i) events[i] = ev[i];
+  gpu_ready = true;
+  return OVVS_STATUS_SUCCESS;
+}
+
+ovvsStatus ovvsResourcesImpl::reserve_workspace(size_t bytes, ovvs::GpuWork& work) {
+  if (workspace.size() >= bytes) return OVVS_STATUS_SUCCESS;
+  (void)hipStreamSynchronize(stream);
+  // Grow geometrically so repeated calls with slowly growing batches settle.
+  size_t want = workspace.size() * 2;
+  if (want < bytes) want = bytes;
+  hipError_t e = workspace.allocate(want);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    e = workspace.allocate(bytes);
+    want = bytes;
+  }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return OVVS_STATUS_OOM;
+  }
+  ovvs::saturating_add(work.allocation_calls, 1);
+  ovvs::saturating_add(work.allocation_bytes, static_cast<int64_t>(want));
+  return OVVS_STATUS_SUCCESS;
+}
+
+ovvsStatus ovvsResourcesImpl::reserve_pinned(size_t bytes) {
+  if (pinned_bytes >= bytes) return OVVS_STATUS_SUCCESS;
+  (void)hipStreamSynchronize(stream);
+  if (pinned) (void)hipHostFree(pinned);
+  pinned = nullptr;
+  pinned_bytes = 0;
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  void* p = nullptr;
+  if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) {
+    (void)hipGetLastError();
+    return OVVS_STATUS_OOM;
+  }
+  pinned = p;
+  pinned_bytes = want;
+  return OVVS_STATUS_SUCCESS;
+}
+
+extern "C" {
+
+OVVS_API const char* ovvsGetVersion(void) { return OVVS_VERSION_STRING; }
+
+OVVS_API const char* ovvsStatusString(ovvsStatus status) {
+  switch (status) {
+    case OVVS_STATUS_SUCCESS:
+      return "success";
+    case OVVS_STATUS_ERROR:
+      return "error";
+    case OVVS_STATUS_INVALID_ARGUMENT:
+      return "invalid argument";
+    case OVVS_STATUS_UNSUPPORTED:
+      return "unsupported";
+    case OVVS_STATUS_OOM:
+      return "out of memory";
+    case OVVS_STATUS_COMPILE_FAIL:
+      return "compile fail";
+    case OVVS_STATUS_SHAPE_MISMATCH:
+      return "shape mismatch";
+    case OVVS_STATUS_DEVICE_UNAVAILABLE:
+      return "device unavailable";
+    case OVVS_STATUS_IO:
+      return "io error";
+  }
+  return "unknown";
+}
+
+OVVS_API ovvsStatus ovvsResourcesCreate(ovvsResources_t* res) {
+  if (!res) return OVVS_STATUS_INVALID_ARGUMENT;
+  auto* r = new (std::nothrow) ovvsResourcesImpl();
+  if (!r) return OVVS_STATUS_OOM;
+  *res = r;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesDestroy(ovvsResources_t res) {
+  delete res;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesSetPolicy(ovvsResources_t res, ovvsPolicy policy) {
+  if (!res) return OVVS_STATUS_INVALID_ARGUMENT;
+  res->policy = policy;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesGetPolicy(ovvsResources_t res, ovvsPolicy* policy) {
+  if (!res || !policy) return OVVS_STATUS_INVALID_ARGUMENT;
+  *policy = res->policy;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesNpuAvailable(ovvsResources_t res, int32_t* available) {
+  if (!res || !available) return OVVS_STATUS_INVALID_ARGUMENT;
+  *available = 0;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesGpuAvailable(ovvsResources_t res, int32_t* available) {
+  if (!res || !available) return OVVS_STATUS_INVALID_ARGUMENT;
+  *available = ovvs::gpu_present() ? 1 : 0;
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesSku(ovvsResources_t res, char* buf, int32_t len) {
+  if (!res || !buf || len <= 0) return OVVS_STATUS_INVALID_ARGUMENT;
+  const char* sku = "generic-cpu";
+  char name[256] = {0};
+  if (ovvs::gpu_present()) {
+    hipDeviceProp_t prop;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess) {
+      std::snprintf(name, sizeof(name), "%s", prop.gcnArchName);
+      sku = name;
+    }
+  }
+  std::snprintf(buf, static_cast<size_t>(len), "%s", sku);
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesLastDevice(ovvsResources_t res, ovvsDevice* device) {
+  if (!res || !device) return OVVS_STATUS_INVALID_ARGUMENT;
+  *device = res->last_device.load();
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesLastComputeDtype(ovvsResources_t res, ovvsDType* dtype) {
+  if (!res || !dtype) return OVVS_STATUS_INVALID_ARGUMENT;
+  *dtype = res->last_compute_dtype.load();
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsResourcesIvfPqSearchStatsV1(ovvsResources_t res,
+                                                    ovvsIvfPqSearchStatsV1* stats) {
+  if (!res || !stats) return OVVS_STATUS_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lock(res->stats_mutex);
+  *stats = res->stats;
+  stats->abi_version = OVVS_IVF_PQ_SEARCH_STATS_ABI_V1;
+  stats->struct_size = static_cast<uint32_t>(sizeof(*stats));
+  return OVVS_STATUS_SUCCESS;
+}
+
+OVVS_API ovvsStatus ovvsBitsetFromAllowList(int64_t n, const int64_t* ids, int64_t nids,
+                                            uint8_t* bitset) {
+  if (!bitset || n <= 0 || nids < 0) return OVVS_STATUS_INVALID_ARGUMENT;
+  const int64_t nbytes = n / 8 + (n % 8 != 0 ? 1 : 0);
+  std::memset(bitset, 0, static_cast<size_t>(nbytes));
+  if (!ids) return OVVS_STATUS_SUCCESS;
+  for (int64_t i = 0; i < nids; ++i) {
+    const int64_t id = ids[i];
+    if (id >= 0 && id < n) bitset[id / 8] = static_cast<uint8_t>(bitset[id / 8] | (1u << (id % 8)));
+  }
+  return OVVS_STATUS_SUCCESS;
+}
+
+}  // extern "C"
+
+static_assert(sizeof(ovvsIvfPqSearchStatsV1) == 200, "ovvsIvfPqSearchStatsV1 is a 200-byte ABI");

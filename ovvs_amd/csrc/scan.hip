@@ -1,0 +1,369 @@
+// scan.hip — fused residual-LUT build + PQ code scan + shortlist select for
+// IVF-PQ search on gfx950.
+//
+// Reference behaviour: for every probed list l of query q (in probe-rank order)
+// the residual r = q - c_l gives the table T[m][j] = sum_u (r[m*dsub+u] -
+// B[m][j][u])^2 (src/neighbors/indexes.cpp:764-785, always L2); each row's ADC
+// score is sum_m T[m][code_m], left to right from +0 (src/prim/mixer.cpp:378-390);
+// the shortlist is the first krefine rows under the total order on (score,
+// dense ordinal) where the ordinal runs over the query's accepted rows in probe
+// order (indexes.cpp:683-712,1019-1066; the reference GPU design for this is
+// src/prim/gpu/backend_gpu.cpp:791-1010).
+//
+// Design (one 256-lane workgroup per query, four wave64s):
+//   * per probed list: residual into LDS, then the whole table into LDS (each
+//     lane computes table entries with the reference's operation order), then
+//     every lane scores one 16-byte-aligned packed row per step with 128-bit
+//     code loads and LDS table gathers;
+//   * each wave keeps its own running top-K as a sorted register list
+//     (64 keys per register row, KPL rows), a 128-slot LDS candidate buffer and
+//     a wave-uniform threshold: rows are appended with ballot/popcount (no
+//     atomics, no block barriers) and the buffer is merged in 64-key batches by
+//     a cross-lane bitonic sort plus a bitonic merge;
+//   * at the end the four wave lists are merged once and the query's K best
+//     (key, packed position) pairs are written out.
+// Keys are (order-preserving score bits << 32 | raw ordinal); raw ordinals count
+// every row of earlier probed lists, which orders accepted rows exactly as the
+// dense ordinal does.
+#include <hip/hip_fp16.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+using namespace ovvs_dev;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kBufCap = 128;
+
+__host__ __device__ constexpr size_t round16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
+
+// Compare-exchange of (k, p) with the lane `s` away; this lane keeps the
+// smaller key when keep_min.
+__device__ __forceinline__ void cx_lane(uint64_t& k, int32_t& p, int s, bool keep_min) {
+  const uint64_t ok = shfl_xor_u64(k, s);
+  const int32_t op = __shfl_xor(p, s, 64);
+  const bool take = keep_min ? (ok < k) : (ok > k);
+  if (take) {
+    k = ok;
+    p = op;
+  }
+}
+
+// Sorts one key per lane ascending across the wave.
+__device__ __forceinline__ void sort64(uint64_t& k, int32_t& p) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int sz = 2; sz <= 64; sz <<= 1) {
+#pragma unroll
+    for (int s = sz >> 1; s > 0; s >>= 1) {
+      const bool asc = (lane & sz) == 0;
+      const bool lower = (lane & s) == 0;
+      cx_lane(k, p, s, lower == asc);
+    }
+  }
+}
+
+// Sorts a bitonic sequence of 64*KPL elements (element e = j*64 + lane)
+// ascending.
+template <int KPL>
+__device__ __forceinline__ void bitonic_merge_asc(uint64_t (&lk)[KPL], int32_t (&lp)[KPL]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = KPL / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      if ((j & s) == 0) {
+        const int o = j | s;
+        if (lk[o] < lk[j]) {
+          const uint64_t tk = lk[j];
+          lk[j] = lk[o];
+          lk[o] = tk;
+          const int32_t tp = lp[j];
+          lp[j] = lp[o];
+          lp[o] = tp;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) cx_lane(lk[j], lp[j], s, (lane & s) == 0);
+  }
+}
+
+// Merges 64 keys (one per lane, sorted ascending) into the sorted list, keeping
+// the 64*KPL smallest.
+template <int KPL>
+__device__ __forceinline__ void merge64(uint64_t (&lk)[KPL], int32_t (&lp)[KPL], uint64_t bk,
+                                        int32_t bp) {
+  const int lane = lane_id();
+  const uint64_t rk = shfl_u64(bk, 63 - lane);
+  const int32_t rp = __shfl(bp, 63 - lane, 64);
+  if (rk < lk[KPL - 1]) {
+    lk[KPL - 1] = rk;
+    lp[KPL - 1] = rp;
+  }
+  bitonic_merge_asc<KPL>(lk, lp);
+}
+
+// Key at element e = K-1 of the sorted list (wave-uniform result).
+template <int KPL>
+__device__ __forceinline__ uint64_t kth_key(const uint64_t (&lk)[KPL], int K) {
+  const int j = (K - 1) >> 6;
+  uint64_t v = lk[0];
+#pragma unroll
+  for (int r = 1; r < KPL; ++r) v = (r == j) ? lk[r] : v;
+  return shfl_u64(v, (K - 1) & 63);
+}
+
+__device__ __forceinline__ float lut_value(const float* lut32, const uint16_t* lut16, bool f16,
+                                           int idx) {
+  return f16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx];
+}
+
+// ADC score of one packed row: sum over m of T[m][code_m], left to right.
+template <bool F16>
+__device__ __forceinline__ float adc_row(const uint8_t* __restrict__ row, int pq_m, int ks_log2,
+                                         const float* lut32, const uint16_t* lut16) {
+  float s = 0.f;
+  int m = 0;
+  for (; m + 16 <= pq_m; m += 16) {
+    const uint4 w = *reinterpret_cast<const uint4*>(row + m);
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const uint32_t code = (wv[b >> 2] >> (8 * (b & 3))) & 0xffu;
+      s = s + lut_value(lut32, lut16, F16, ((m + b) << ks_log2) + static_cast<int>(code));
+    }
+  }
+  if (m < pq_m) {
+    const uint4 w = *reinterpret_cast<const uint4*>(row + m);
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    for (int b = 0; m + b < pq_m; ++b) {
+      const uint32_t code = (wv[b >> 2] >> (8 * (b & 3))) & 0xffu;
+      s = s + lut_value(lut32, lut16, F16, ((m + b) << ks_log2) + static_cast<int>(code));
+    }
+  }
+  return s;
+}
+
+struct ScanLayout {
+  size_t lut_bytes;    // table region, also reused for the final cross-wave merge
+  size_t resid_off;
+  size_t bufk_off;
+  size_t bufp_off;
+  size_t total;
+};
+
+__host__ __device__ inline ScanLayout scan_layout(int pq_m, int ks, int dim, int f16, int kpl) {
+  ScanLayout L;
+  const size_t table = round16(static_cast<size_t>(pq_m) * ks * (f16 ? 2u : 4u));
+  const size_t merge = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
+  L.lut_bytes = table > merge ? table : merge;
+  L.resid_off = L.lut_bytes;
+  L.bufk_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
+  L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
+  L.total = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
+  return L;
+}
+
+template <int KPL, bool F16>
+__global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const ScanLayout L = scan_layout(a.pq_m, a.ks, a.dim, F16 ? 1 : 0, KPL);
+  float* lut32 = reinterpret_cast<float*>(smem);
+  uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem);
+  float* resid = reinterpret_cast<float*>(smem + L.resid_off);
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
+  int32_t* bufp = reinterpret_cast<int32_t*>(smem + L.bufp_off) + wave * kBufCap;
+
+  const int64_t q = blockIdx.x;
+  const float* __restrict__ qv = a.queries + q * a.dim;
+  const int lut_n = a.pq_m * a.ks;
+  const int ks_log2 = __ffs(a.ks) - 1;
+  const int K = a.K;
+
+  uint64_t lk[KPL];
+  int32_t lp[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    lk[j] = kNoKey;
+    lp[j] = -1;
+  }
+  uint64_t thr = kNoKey;
+  int cnt = 0;
+  uint32_t ord_base = 0;
+  unsigned long long rows_total = 0, tasks = 0;
+
+  for (int p = 0; p < a.P; ++p) {
+    const int l = a.probes[q * a.P + p];
+    const int64_t begin = a.list_offsets[l];
+    const int64_t rows = a.list_offsets[l + 1] - begin;
+    if (rows <= 0) continue;
+    ++tasks;
+    rows_total += static_cast<unsigned long long>(rows);
+
+    __syncthreads();  // the previous list's scan no longer reads the table
+    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
+    for (int t = threadIdx.x; t < a.dim; t += kThreads) resid[t] = qv[t] - cv[t];
+    __syncthreads();
+    for (int e = threadIdx.x; e < lut_n; e += kThreads) {
+      const float* r = resid + (e >> ks_log2) * a.dsub;
+      const float* __restrict__ b = a.codebooks + static_cast<int64_t>(e) * a.dsub;
+      float s = 0.f;
+      for (int u = 0; u < a.dsub; ++u) {
+        const float d = r[u] - b[u];
+        s = s + d * d;
+      }
+      if (F16) {
+        lut16[e] = __half_as_ushort(__float2half_rn(s));
+      } else {
+        lut32[e] = s;
+      }
+    }
+    __syncthreads();
+
+    for (int64_t r0 = 0; r0 < rows; r0 += kThreads) {
+      const int64_t r = r0 + threadIdx.x;
+      const int64_t pos = begin + r;
+      bool valid = r < rows;
+      if (valid && a.bitset) {
+        const int64_t id = a.ids[pos];
+        valid = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
+      }
+      uint64_t key = kNoKey;
+      if (valid) {
+        const float s = adc_row<F16>(a.codes + pos * a.code_stride, a.pq_m, ks_log2, lut32, lut16);
+        key = make_key(s, ord_base + static_cast<uint32_t>(r));
+      }
+      const bool pass = key < thr;
+      const uint64_t bal = __ballot(pass);
+      if (bal) {
+        const int before = __popcll(bal & ((1ull << lane) - 1ull));
+        if (pass) {
+          bufk[cnt + before] = key;
+          bufp[cnt + before] = static_cast<int32_t>(pos);
+        }
+        cnt += __popcll(bal);
+        if (cnt >= 64) {
+          uint64_t bk = bufk[lane];
+          int32_t bp = bufp[lane];
+          const int rest = cnt - 64;
+          if (lane < rest) {
+            const uint64_t mk = bufk[64 + lane];
+            const int32_t mp = bufp[64 + lane];
+            bufk[lane] = mk;
+            bufp[lane] = mp;
+          }
+          cnt = rest;
+          sort64(bk, bp);
+          merge64<KPL>(lk, lp, bk, bp);
+          thr = kth_key<KPL>(lk, K);
+        }
+      }
+    }
+    ord_base += static_cast<uint32_t>(rows);
+  }
+  if (cnt > 0) {
+    uint64_t bk = lane < cnt ? bufk[lane] : kNoKey;
+    int32_t bp = lane < cnt ? bufp[lane] : -1;
+    sort64(bk, bp);
+    merge64<KPL>(lk, lp, bk, bp);
+  }
+
+  // Cross-wave merge: each wave publishes its sorted list, wave 0 folds in the rest.
+  constexpr int M = 64 * KPL;
+  __syncthreads();
+  uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
+  int32_t* mp = reinterpret_cast<int32_t*>(smem + static_cast<size_t>(kWaves) * M * 8);
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    mk[wave * M + j * 64 + lane] = lk[j];
+    mp[wave * M + j * 64 + lane] = lp[j];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    for (int w = 1; w < kWaves; ++w) {
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int src = w * M + (KPL - 1 - j) * 64 + (63 - lane);
+        const uint64_t rk = mk[src];
+        if (rk < lk[j]) {
+          lk[j] = rk;
+          lp[j] = mp[src];
+        }
+      }
+      bitonic_merge_asc<KPL>(lk, lp);
+    }
+    int valid = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int e = j * 64 + lane;
+      if (e < K) {
+        a.out_keys[q * K + e] = lk[j];
+        a.out_pos[q * K + e] = lp[j];
+        valid += lk[j] != kNoKey;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
+    if (lane == 0) {
+      a.out_count[q] = valid;
+      atomicAdd(&a.counters[0], rows_total);
+      atomicAdd(&a.counters[1], tasks);
+      atomicAdd(&a.counters[2], static_cast<unsigned long long>(valid));
+    }
+  }
+}
+
+template <int KPL, bool F16>
+hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
+  auto fn = k_scan<KPL, F16>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(a.nq)), dim3(kThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+int kpl_for(int K) { return K <= 64 ? 1 : (K <= 128 ? 2 : 4); }
+
+}  // namespace
+
+extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
+                                          int32_t lut_f16) {
+  if (pq_m <= 0 || ks <= 0 || dim <= 0) return 0;
+  const size_t b = scan_layout(pq_m, ks, dim, lut_f16 ? 1 : 0, 4).total;
+  return b <= 160u * 1024u ? b : 0;
+}
+
+extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream) {
+  if (!args) return hipErrorInvalidValue;
+  const OvvsScanArgs& a = *args;
+  if (a.nq <= 0) return hipSuccess;
+  if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
+      !a.ids || !a.out_keys || !a.out_pos || !a.out_count || !a.counters || a.nq > 0x7fffffff ||
+      a.dim <= 0 || a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 ||
+      (a.ks & (a.ks - 1)) != 0 || a.code_stride < a.pq_m || (a.code_stride & 15) != 0 ||
+      static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
+    return hipErrorInvalidValue;
+  const int kpl = kpl_for(a.K);
+  const size_t lds = scan_layout(a.pq_m, a.ks, a.dim, a.lut_f16 ? 1 : 0, kpl).total;
+  if (lds > 160u * 1024u) return hipErrorInvalidValue;
+  if (a.lut_f16) {
+    if (kpl == 1) return launch_scan<1, true>(a, lds, stream);
+    if (kpl == 2) return launch_scan<2, true>(a, lds, stream);
+    return launch_scan<4, true>(a, lds, stream);
+  }
+  if (kpl == 1) return launch_scan<1, false>(a, lds, stream);
+  if (kpl == 2) return launch_scan<2, false>(a, lds, stream);
+  return launch_scan<4, false>(a, lds, stream);
+}

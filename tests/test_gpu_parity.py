@@ -1,0 +1,266 @@
+"""GPU parity: libovvs on the MI355X against the reference and the oracle.
+
+Bar (north star): neighbor ids identical to the reference's, distances within
+1e-4 relative for fp32 tables (2e-3 for binary16 tables); every comparison here
+also checks that the fp32 path is bit-identical, which is what the kernels are
+built for (separately rounded fp32 in the reference's order).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import sys
+import threading
+
+import numpy as np
+import pytest
+
+from conftest import assert_results_match, case_data, write_case_ipq1
+from oracle.pyoracle import REF_SO, Oracle, Reference, read_ipq1
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+@pytest.fixture(scope="module")
+def res(ovvs):
+    r = ovvs.Resources()
+    if not r.gpu_available():
+        pytest.fail("no GPU visible: gpu tests must run on the MI355X box")
+    return r
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_reference_cases_bit_exact(ovvs, res, ref_cases, tmp_path):
+    manifest, arrays = ref_cases
+    for case in manifest:
+        say("case", case["name"])
+        ix = ovvs.neighbors.ivf_pq.load(write_case_ipq1(case, arrays, tmp_path), resources=res)
+        q = arrays[f"{case['name']}/queries"]
+        for j, s in enumerate(case["searches"]):
+            key = f"{case['name']}/s{j}"
+            ids, d = ix.search(q, s["k"], s["nprobe"], s["krefine"],
+                               bitset=arrays.get(f"{key}/bitset"))
+            assert_results_match(ids, d, arrays[f"{key}/ids"], arrays[f"{key}/dists"], label=key)
+            assert np.array_equal(_bits(d), _bits(arrays[f"{key}/dists"])), key
+        ix.close()
+
+
+def test_legacy_ipq1_on_gpu(ovvs, res):
+    from conftest import GOLDEN
+
+    ix = ovvs.neighbors.ivf_pq.load(GOLDEN / "legacy_ipq1_v1.bin", resources=res)
+    ids, d = ix.search(np.array([[1.1, 0.0]], np.float32), k=2, nprobe=1, krefine=4)
+    assert ids.tolist() == [[1, 2]]
+    assert abs(d[0, 0] - 0.01) < 1e-5 and abs(d[0, 1] - 0.81) < 1e-5
+
+
+def test_gpu_build_matches_reference_build_bytes(ovvs, res, ref_cases, tmp_path):
+    """ovvsIvfPqBuild (+Extend) on the GPU against the reference's own build on the
+    same inputs: k-means seeding, assignment, row-order means and encoding are
+    reproduced exactly, so the serialized indexes must be byte-identical."""
+    manifest, arrays = ref_cases
+    for case in manifest:
+        data = case_data(case, arrays)
+        say("build", case["name"], data.shape)
+        ix = ovvs.neighbors.ivf_pq.build(data, metric=case["metric"], nlist=case["nlist"],
+                                         pq_m=case["pq_m"], pq_nbits=case["nbits"], resources=res)
+        if case["extended"]:
+            ix.extend(case_data(case, arrays, "extra"))
+        out = tmp_path / "ours.ipq1"
+        ix.serialize(out)
+        ours = read_ipq1(out)
+        theirs = read_ipq1(write_case_ipq1(case, arrays, tmp_path))
+        assert np.array_equal(_bits(ours.centroids), _bits(theirs.centroids)), case["name"]
+        assert np.array_equal(_bits(ours.codebooks), _bits(theirs.codebooks)), case["name"]
+        assert np.array_equal(ours.assign, theirs.assign), case["name"]
+        assert np.array_equal(ours.codes, theirs.codes), case["name"]
+        assert out.read_bytes() == arrays[f"{case['name']}/ipq1"].tobytes(), case["name"]
+        ix.close()
+
+
+def test_fp16_tables_match_oracle_extension(ovvs, res, ref_cases, tmp_path):
+    manifest, arrays = ref_cases
+    for name in ("mid8", "mid4", "metric0", "metric2", "filters"):
+        case = next(c for c in manifest if c["name"] == name)
+        say("fp16", name)
+        path = write_case_ipq1(case, arrays, tmp_path)
+        orc = Oracle(read_ipq1(path))
+        ix = ovvs.neighbors.ivf_pq.load(path, resources=res)
+        q = arrays[f"{name}/queries"]
+        for j, s in enumerate(case["searches"]):
+            bits = arrays.get(f"{name}/s{j}/bitset")
+            ids, d = ix.search_ex(q, s["k"], s["nprobe"], s["krefine"], bitset=bits,
+                                  lut_dtype=ovvs.DTYPE_F16)
+            oids, od = orc.search(q, s["k"], s["nprobe"], s["krefine"], bits, lut_f16=True)
+            assert_results_match(ids, d, oids, od, rel=2e-3, label=f"{name}/s{j}")
+            assert np.array_equal(_bits(d), _bits(od))
+        ix.close()
+    assert res.last_compute_dtype() == ovvs.DTYPE_F16
+
+
+def test_random_indexes_against_oracle(ovvs, res, tmp_path):
+    rng = np.random.default_rng(11)
+    for trial in range(6):
+        dim = int(rng.choice([8, 16, 24, 48, 96]))
+        pq_m = int(rng.choice([d for d in (1, 2, 3, 4, 8, 12, 16, 24, 32, 48) if dim % d == 0]))
+        n = int(rng.integers(500, 6000))
+        nlist = int(rng.integers(4, 96))
+        nbits = int(rng.choice([4, 5, 8]))
+        metric = int(rng.integers(0, 6))
+        say("trial", trial, dict(n=n, dim=dim, pq_m=pq_m, nlist=nlist, nbits=nbits, metric=metric))
+        centers = rng.standard_normal((32, dim)).astype(np.float32)
+        data = (centers[rng.integers(0, 32, n)] +
+                0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+        q = (centers[rng.integers(0, 32, 100)] +
+             0.3 * rng.standard_normal((100, dim))).astype(np.float32)
+        ix = ovvs.neighbors.ivf_pq.build(data, metric=metric, nlist=nlist, pq_m=pq_m,
+                                         pq_nbits=nbits, resources=res)
+        p = tmp_path / "rand.ipq1"
+        ix.serialize(p)
+        orc = Oracle(read_ipq1(p))
+        bitset = np.packbits((rng.random(n) < 0.7).astype(np.uint8), bitorder="little")
+        for k, nprobe, krefine, bits in [(10, 8, 10, None), (10, 4, 64, None), (1, 1, 1, None),
+                                         (32, nlist, 200, None), (10, 6, 40, bitset),
+                                         (256, 3, 256, None)]:
+            ids, d = ix.search(q, k, nprobe, krefine, bitset=bits)
+            oids, od = orc.search(q, k, nprobe, krefine, bits)
+            assert_results_match(ids, d, oids, od, label=f"trial{trial} k{k} p{nprobe} r{krefine}")
+            assert np.array_equal(_bits(d), _bits(od))
+        ix.close()
+
+
+def test_device_pointer_entry_matches_host_entry(ovvs, res, ref_cases, tmp_path):
+    import torch
+
+    manifest, arrays = ref_cases
+    case = next(c for c in manifest if c["name"] == "mid8")
+    ix = ovvs.neighbors.ivf_pq.load(write_case_ipq1(case, arrays, tmp_path), resources=res)
+    q = arrays["mid8/queries"]
+    ids, d = ix.search(q, 10, 8, 32)
+    dq = torch.from_numpy(q).to("cuda:0")
+    did = torch.empty((q.shape[0], 10), dtype=torch.int64, device="cuda:0")
+    dd = torch.empty((q.shape[0], 10), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    ix.search_device(dq.data_ptr(), q.shape[0], 10, 8, 32, did.data_ptr(), dd.data_ptr())
+    assert np.array_equal(did.cpu().numpy(), ids)
+    assert np.array_equal(_bits(dd.cpu().numpy()), _bits(d))
+    ix.close()
+
+
+def test_batch_independence_and_determinism(ovvs, res, ref_cases, tmp_path):
+    manifest, arrays = ref_cases
+    case = next(c for c in manifest if c["name"] == "mid8")
+    ix = ovvs.neighbors.ivf_pq.load(write_case_ipq1(case, arrays, tmp_path), resources=res)
+    q = arrays["mid8/queries"]
+    full_ids, full_d = ix.search(q, 10, 8, 32)
+    same = np.repeat(q[:1], 33, axis=0)
+    ids33, d33 = ix.search(same, 10, 8, 32)
+    assert np.all(ids33 == full_ids[0]) and np.all(_bits(d33) == _bits(full_d[0]))
+    for lo, hi in [(0, 1), (5, 37), (37, 64)]:
+        ids, d = ix.search(q[lo:hi], 10, 8, 32)
+        assert np.array_equal(ids, full_ids[lo:hi])
+    again_ids, again_d = ix.search(q, 10, 8, 32)
+    assert np.array_equal(again_ids, full_ids) and np.array_equal(_bits(again_d), _bits(full_d))
+    ix.close()
+
+
+def test_concurrent_searches_share_one_index(ovvs, ref_cases, tmp_path):
+    manifest, arrays = ref_cases
+    case = next(c for c in manifest if c["name"] == "mid8")
+    path = write_case_ipq1(case, arrays, tmp_path)
+    owner = ovvs.Resources()
+    ix = ovvs.neighbors.ivf_pq.load(path, resources=owner)
+    q = arrays["mid8/queries"]
+    want = ix.search(q, 10, 8, 32)
+    results = {}
+
+    def worker(t):
+        r = ovvs.Resources()
+        h = ix._h
+        ids = np.empty((q.shape[0], 10), np.int64)
+        d = np.empty((q.shape[0], 10), np.float32)
+        rcs = []
+        for _ in range(5):
+            rcs.append(ovvs._lib.ovvsIvfPqSearch(
+                r._h, h, q.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), q.shape[0], 10, 8, 32,
+                None, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                d.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        results[t] = (rcs, ids.copy(), d.copy())
+        r.close()
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for rcs, ids, d in results.values():
+        assert rcs == [0] * 5
+        assert np.array_equal(ids, want[0]) and np.array_equal(_bits(d), _bits(want[1]))
+    ix.close()
+
+
+def test_telemetry_counts_and_failure_atomicity(ovvs, res, ref_cases, tmp_path):
+    manifest, arrays = ref_cases
+    case = next(c for c in manifest if c["name"] == "mid8")
+    path = write_case_ipq1(case, arrays, tmp_path)
+    r = ovvs.Resources()
+    ix = ovvs.neighbors.ivf_pq.load(path, resources=r)
+    orc = Oracle(read_ipq1(path))
+    q = arrays["mid8/queries"]
+    before = r.ivfpq_search_stats()
+    ix.search(q, 10, 8, 32)
+    after = r.ivfpq_search_stats()
+    probes = orc.probes(q, 8)
+    sizes = np.diff(orc.offsets)
+    rows = int(sizes[probes].sum())
+    tasks = int((sizes[probes] > 0).sum())
+    assert after["successful_calls"] - before["successful_calls"] == 1
+    assert after["queries"] - before["queries"] == q.shape[0]
+    assert after["candidate_rows"] - before["candidate_rows"] == rows
+    assert after["tasks"] - before["tasks"] == tasks
+    assert after["selected_rows"] - before["selected_rows"] == q.shape[0] * 32
+    assert after["adc_scan_select_ns"] > before["adc_scan_select_ns"]
+    assert after["gpu_kernel_launches"] > before["gpu_kernel_launches"]
+    assert r.last_device() == ovvs.DEVICE_GPU
+    with pytest.raises(ovvs.OvvsError):
+        ix.search(q, 10, 8, 1000)  # krefine beyond the register list
+    assert r.ivfpq_search_stats() == after
+    ix.close()
+
+
+@pytest.mark.skipif(not REF_SO.exists(), reason="oracle/_ref not built")
+def test_c1_scale_against_reference(ovvs, res, tmp_path):
+    """Config 1 (100k x 128, 256 lists, pq 32, 16 probes, k 10, fp32 tables): the
+    quantizers are trained on the 20k-row prefix, the rest is appended with
+    extend; the reference library searches the same serialized index."""
+    from ovvs_amd import synth
+
+    cfg = synth.CONFIGS["c1"]
+    C = synth.centers(cfg)
+    data = synth.base_rows(cfg, 0, cfg.n, C)
+    q = synth.query_rows(cfg, 0, 200, C)
+    say("c1 build")
+    ix = ovvs.neighbors.ivf_pq.build(data[:cfg.train_rows], nlist=cfg.nlist, pq_m=cfg.pq_m,
+                                     resources=res)
+    ix.extend(data[cfg.train_rows:])
+    p = tmp_path / "c1.ipq1"
+    ix.serialize(p)
+    say("c1 search")
+    ids, d = ix.search(q, cfg.k, cfg.nprobe, cfg.k)
+    ref = Reference()
+    rc, h = ref.load(p)
+    assert rc == 0
+    rc, rids, rd = ref.search(h, q, cfg.k, cfg.nprobe, cfg.k)
+    assert rc == 0
+    assert_results_match(ids, d, rids, rd, label="c1")
+    assert np.array_equal(_bits(d), _bits(rd))
+    ref.destroy(h)
+    ref.close()
+    ix.close()
