@@ -108,8 +108,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
   const int lut_f16 = lut_dtype == OVVS_DTYPE_F16 ? 1 : 0;
   // Fixed limits of the kernels: fail closed, as the reference's GPU route does
   // for krefine > 128 (indexes.cpp:576-584).
+  // OVVS_HIP_MAX_REFINE bounds krefine and k.
   if (R > OVVS_HIP_MAX_REFINE || P > OVVS_HIP_MAX_PROBES ||
-      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16) == 0 ||
+      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16, R) == 0 ||
       nq > 0x7fffffff) {
     return OVVS_STATUS_DEVICE_UNAVAILABLE;
   }

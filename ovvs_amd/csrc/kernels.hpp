@@ -14,8 +14,8 @@ extern "C" {
 #endif
 
 // Largest shortlist (krefine) and final k the scan/refine kernels hold in
-// registers: 64 keys per lane-row, up to 4 rows per wave.
-#define OVVS_HIP_MAX_REFINE 256
+// registers: 64 keys per register row, up to 16 rows per wave.
+#define OVVS_HIP_MAX_REFINE 1024
 // Largest probe count the in-LDS probe selection sorts (32 KiB of 64-bit keys).
 #define OVVS_HIP_MAX_PROBES 4096
 
@@ -69,8 +69,9 @@ struct OvvsScanArgs {
 // Fused residual-LUT build (in LDS) + ADC code scan + per-query shortlist of
 // the K best (ADC score, dense ordinal) rows over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
-// Dynamic LDS bytes the scan kernel needs for these shapes (0 if unsupported).
-size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16);
+// Dynamic LDS bytes the scan kernel needs for these shapes and shortlist
+// length (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
+size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K);
 
 struct OvvsRefineArgs {
   const float* queries;   // [nq * dim]

@@ -30,23 +30,32 @@ __device__ float metric_value(int metric, const float* __restrict__ q,
     case kIP:
       return -seq_dot(q, x, dim);
     case kCosine: {
+      // __builtin_sqrtf and '/' lower to correctly rounded sequences (no
+      // fast-math, no approximate-sqrt flags), as x86 sqrtss/divss are.
       const float ip = seq_dot(q, x, dim);
-      const float a = __fsqrt_rn(ref_max(qn, 1e-12f));
-      const float b = __fsqrt_rn(ref_max(xn, 1e-12f));
-      return 1.f - __fdiv_rn(ip, a * b);
+      const float a = __builtin_sqrtf(ref_max(qn, 1e-12f));
+      const float b = __builtin_sqrtf(ref_max(xn, 1e-12f));
+      return 1.f - ip / (a * b);
     }
     case kL2Sqrt:
-      return __fsqrt_rn(seq_l2sq(q, x, dim));
+      return __builtin_sqrtf(seq_l2sq(q, x, dim));
     case kHamming: {
       int s = 0;
       for (int i = 0; i < dim; ++i) s += static_cast<int>((q[i] >= 0.f) != (x[i] >= 0.f));
       return static_cast<float>(s);
     }
     case kLp: {
-      // Minkowski p = 2 as the search passes it (reference indexes.cpp:1076).
+      // Minkowski p = 2 as the search passes it (reference indexes.cpp:1076):
+      // (sum |q-x|^2)^(1/2). The reference evaluates both powers with powf;
+      // |t|^2 and s^(1/2) are computed here as the correctly rounded t*t and
+      // sqrt(s), which powf returns too except when its result lies within its
+      // own error bound of a rounding midpoint.
       float s = 0.f;
-      for (int i = 0; i < dim; ++i) s = s + powf(fabsf(q[i] - x[i]), 2.f);
-      return powf(s, 0.5f);
+      for (int i = 0; i < dim; ++i) {
+        const float t = fabsf(q[i] - x[i]);
+        s = s + t * t;
+      }
+      return __builtin_sqrtf(s);
     }
     default:
       return seq_l2sq(q, x, dim);

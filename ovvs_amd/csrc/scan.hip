@@ -334,14 +334,14 @@ hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   return hipGetLastError();
 }
 
-int kpl_for(int K) { return K <= 64 ? 1 : (K <= 128 ? 2 : 4); }
+int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512 ? 8 : 16; }
 
 }  // namespace
 
 extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
-                                          int32_t lut_f16) {
-  if (pq_m <= 0 || ks <= 0 || dim <= 0) return 0;
-  const size_t b = scan_layout(pq_m, ks, dim, lut_f16 ? 1 : 0, 4).total;
+                                          int32_t lut_f16, int32_t K) {
+  if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE) return 0;
+  const size_t b = scan_layout(pq_m, ks, dim, lut_f16 ? 1 : 0, kpl_for(K)).total;
   return b <= 160u * 1024u ? b : 0;
 }
 
@@ -359,11 +359,19 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   const size_t lds = scan_layout(a.pq_m, a.ks, a.dim, a.lut_f16 ? 1 : 0, kpl).total;
   if (lds > 160u * 1024u) return hipErrorInvalidValue;
   if (a.lut_f16) {
-    if (kpl == 1) return launch_scan<1, true>(a, lds, stream);
-    if (kpl == 2) return launch_scan<2, true>(a, lds, stream);
-    return launch_scan<4, true>(a, lds, stream);
+    switch (kpl) {
+      case 1: return launch_scan<1, true>(a, lds, stream);
+      case 2: return launch_scan<2, true>(a, lds, stream);
+      case 4: return launch_scan<4, true>(a, lds, stream);
+      case 8: return launch_scan<8, true>(a, lds, stream);
+      default: return launch_scan<16, true>(a, lds, stream);
+    }
   }
-  if (kpl == 1) return launch_scan<1, false>(a, lds, stream);
-  if (kpl == 2) return launch_scan<2, false>(a, lds, stream);
-  return launch_scan<4, false>(a, lds, stream);
+  switch (kpl) {
+    case 1: return launch_scan<1, false>(a, lds, stream);
+    case 2: return launch_scan<2, false>(a, lds, stream);
+    case 4: return launch_scan<4, false>(a, lds, stream);
+    case 8: return launch_scan<8, false>(a, lds, stream);
+    default: return launch_scan<16, false>(a, lds, stream);
+  }
 }

@@ -13,6 +13,14 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+try:
+    # libovvs and torch-ROCm each bring a libamdhip64.so.7; the first one loaded
+    # serves the whole process. Loading torch's first keeps torch usable in the
+    # GPU tests that allocate device memory through it.
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = Path(__file__).resolve().parents[1]
 GOLDEN = ROOT / "tests" / "golden"
 if str(ROOT) not in sys.path:

@@ -202,13 +202,13 @@ def test_search_argument_checks_leave_outputs_untouched(ovvs):
         ((res, h, q, 1, 0, 1, 4), INV),            # k <= 0
         ((res, h, q, 1, 2**31, 1, 4), INV),        # k > INT32_MAX
         ((res, h, q, 2**62, 2**30, 1, 4), SHAPE),  # nq * k overflows
-        ((res, h, q, 1, 2, 1, 257), DEV),          # krefine beyond the kernels' register list
-        ((res, h, q, 1, 300, 1, 4), DEV),          # k beyond it as well
+        ((res, h, q, 1, 2, 1, 1025), DEV),         # krefine beyond the kernels' register list
+        ((res, h, q, 1, 1100, 1, 4), DEV),         # k beyond it as well
     ]
     for args, want in cases:
         r, hh, qq, nq, k, nprobe, kr = args
-        ids = np.full(4, 7, dtype=np.int64)
-        d = np.full(4, -3.0, dtype=np.float32)
+        ids = np.full(1200, 7, dtype=np.int64)
+        d = np.full(1200, -3.0, dtype=np.float32)
         qp = None if qq is None else qq.ctypes.data_as(POINTER(c_float))
         rc = ovvs._lib.ovvsIvfPqSearch(r._h if r else None, hh, qp, c_int64(nq), c_int64(k),
                                        c_int32(nprobe), c_int32(kr), None,
