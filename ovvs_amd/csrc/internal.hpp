@@ -46,16 +46,16 @@ class DeviceBuffer {
   size_t bytes_ = 0;
 };
 
-// Device copy of an index. Codes are list-major with each row padded to
-// code_stride bytes (a multiple of 16) so the scan issues aligned 128-bit loads;
-// ids are list-major; offsets are the list CSR; dataset rows are by id.
+// Device copy of an index. Codes are list-major in the tiled block layout of
+// kernels.hpp (OVVS_CODE_TILE_ROWS); ids are list-major; offsets are the list
+// CSR; dataset rows are by id.
 struct IndexDevice {
   int device = -1;
-  int32_t code_stride = 0;
+  int32_t code_blocks = 0;
   DeviceBuffer centroids;  // [nlist * dim] f32
   DeviceBuffer cnorm;      // [nlist] f32
   DeviceBuffer codebooks;  // [pq_m * ks * dsub] f32
-  DeviceBuffer codes;      // [n * code_stride] u8
+  DeviceBuffer codes;      // [ceil(n / 64) * code_blocks * 512] u8
   DeviceBuffer ids;        // [n] i64
   DeviceBuffer offsets;    // [nlist + 1] i64
   DeviceBuffer dataset;    // [n * dim] f32

@@ -272,17 +272,22 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
   if (!ovvs::lists_valid(*this)) return OVVS_STATUS_ERROR;
   auto d = std::make_unique<ovvs::IndexDevice>();
   d->device = res.device;
-  d->code_stride = (pq_m + 15) & ~15;
-  const size_t stride = static_cast<size_t>(d->code_stride);
+  constexpr size_t kB = OVVS_CODE_BLOCK, kT = OVVS_CODE_TILE_ROWS;
+  const size_t nblocks = (static_cast<size_t>(pq_m) + kB - 1) / kB;
+  d->code_blocks = static_cast<int32_t>(nblocks);
+  const size_t tiles = (static_cast<size_t>(n) + kT - 1) / kT;
   std::vector<int64_t> offsets(static_cast<size_t>(nlist) + 1, 0);
   std::vector<int64_t> ids(static_cast<size_t>(n));
-  std::vector<uint8_t> packed(static_cast<size_t>(n) * stride, 0);
+  std::vector<uint8_t> packed(tiles * nblocks * kT * kB, 0);
   size_t pos = 0;
   for (int32_t c = 0; c < nlist; ++c) {
     for (const int64_t id : lists[static_cast<size_t>(c)]) {
       ids[pos] = id;
-      std::memcpy(packed.data() + pos * stride, codes.data() + static_cast<size_t>(id) * pq_m,
-                  static_cast<size_t>(pq_m));
+      const uint8_t* src = codes.data() + static_cast<size_t>(id) * pq_m;
+      uint8_t* tile = packed.data() + (pos / kT) * (nblocks * kT * kB) + (pos % kT) * kB;
+      for (size_t m = 0; m < static_cast<size_t>(pq_m); ++m) {
+        tile[(m / kB) * (kT * kB) + (m % kB)] = src[m];
+      }
       ++pos;
     }
     offsets[static_cast<size_t>(c) + 1] = static_cast<int64_t>(pos);

@@ -199,7 +199,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.pq_m = ix.pq_m;
     sa.ks = ix.pq_ks;
     sa.dsub = ix.dsub;
-    sa.code_stride = dv.code_stride;
+    sa.code_blocks = dv.code_blocks;
     sa.list_offsets = dv.offsets.as<int64_t>();
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();

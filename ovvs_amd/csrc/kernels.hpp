@@ -19,6 +19,15 @@ extern "C" {
 // Largest probe count the in-LDS probe selection sorts (32 KiB of 64-bit keys).
 #define OVVS_HIP_MAX_PROBES 4096
 
+// Device layout of the packed PQ codes. Rows keep the list-major order of the
+// reference's packed CSR (packed position p); they are grouped in tiles of
+// OVVS_CODE_TILE_ROWS rows, and inside a tile the codes of subspace block b
+// (OVVS_CODE_BLOCK subspaces, one byte each, zero-padded past pq_m) of the
+// tile's rows are contiguous:
+//   offset(p, b) = (p / 64) * (nblocks * 64 * 8) + b * (64 * 8) + (p % 64) * 8.
+#define OVVS_CODE_BLOCK 8
+#define OVVS_CODE_TILE_ROWS 64
+
 // out[i] = sum_t x[i*dim+t]^2, left to right from +0 (reference internal.hpp:221-225).
 hipError_t ovvs_hip_row_norms(const float* x, int64_t n, int32_t dim, float* out,
                               hipStream_t stream);
@@ -52,9 +61,9 @@ struct OvvsScanArgs {
   int32_t pq_m;
   int32_t ks;                  // power of two, 16..256
   int32_t dsub;
-  int32_t code_stride;         // bytes per packed row, multiple of 16
+  int32_t code_blocks;         // ceil(pq_m / OVVS_CODE_BLOCK)
   const int64_t* list_offsets; // [nlist + 1]
-  const uint8_t* codes;        // [n * code_stride], list-major
+  const uint8_t* codes;        // tiled list-major codes, see OVVS_CODE_TILE_ROWS
   const int64_t* ids;          // [n], list-major
   const uint8_t* bitset;       // (n+7)/8 bytes or nullptr
   int32_t K;                   // shortlist length (krefine), 1..OVVS_HIP_MAX_REFINE

@@ -7,21 +7,29 @@
 // score is sum_m T[m][code_m], left to right from +0 (src/prim/mixer.cpp:378-390);
 // the shortlist is the first krefine rows under the total order on (score,
 // dense ordinal) where the ordinal runs over the query's accepted rows in probe
-// order (indexes.cpp:683-712,1019-1066; the reference GPU design for this is
-// src/prim/gpu/backend_gpu.cpp:791-1010).
+// order (indexes.cpp:683-712,1019-1066; the reference's own GPU design for this
+// step is src/prim/gpu/backend_gpu.cpp:791-1010).
 //
 // Design (one 256-lane workgroup per query, four wave64s):
-//   * per probed list: residual into LDS, then the whole table into LDS (each
-//     lane computes table entries with the reference's operation order), then
-//     every lane scores one 16-byte-aligned packed row per step with 128-bit
-//     code loads and LDS table gathers;
-//   * each wave keeps its own running top-K as a sorted register list
-//     (64 keys per register row, KPL rows), a 128-slot LDS candidate buffer and
-//     a wave-uniform threshold: rows are appended with ballot/popcount (no
-//     atomics, no block barriers) and the buffer is merged in 64-key batches by
-//     a cross-lane bitonic sort plus a bitonic merge;
-//   * at the end the four wave lists are merged once and the query's K best
-//     (key, packed position) pairs are written out.
+//   * Rows are processed in chunks of up to 4096 (16 per lane, partial sums in
+//     registers) and subspaces in blocks of 8. For each block the workgroup
+//     builds only that block's 8 x ks table slice into LDS (each entry with the
+//     reference's operation order), then every live row adds its 8 entries in
+//     order m = 8b..8b+7.
+//   * Table entries are squared distances (>= +0, or NaN), so fp32 partial sums
+//     never decrease. A row whose partial sum already exceeds the K-th best key
+//     of any wave (each such key has K better rows behind it) cannot enter the
+//     shortlist and is dropped; when a block has no live row left the remaining
+//     blocks (their table slices and their code bytes) are skipped. Surviving
+//     rows are scored completely, so the shortlist is exactly the reference's.
+//   * Codes are stored tiled: 64-row tiles, inside a tile 8-byte slabs of one
+//     block for 64 consecutive rows, so a wave's block load is one coalesced
+//     512-byte access and skipped blocks are never fetched.
+//   * Each wave keeps its own running top-K as a sorted register list (64 keys
+//     per register row, KPL rows), a 128-slot LDS candidate buffer and a
+//     threshold it publishes in LDS: rows are appended with ballot/popcount (no
+//     atomics), buffers are merged by a cross-lane bitonic sort plus a bitonic
+//     merge, and at the end the four lists are merged once.
 // Keys are (order-preserving score bits << 32 | raw ordinal); raw ordinals count
 // every row of earlier probed lists, which orders accepted rows exactly as the
 // dense ordinal does.
@@ -37,6 +45,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kBufCap = 128;
+constexpr int kRowsPerLane = 8;
+constexpr int kChunkRows = kThreads * kRowsPerLane;
+constexpr int kBlock = OVVS_CODE_BLOCK;      // subspaces per block (8)
+constexpr int kTile = OVVS_CODE_TILE_ROWS;   // rows per code tile (64)
 
 __host__ __device__ constexpr size_t round16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
 
@@ -120,52 +132,29 @@ __device__ __forceinline__ uint64_t kth_key(const uint64_t (&lk)[KPL], int K) {
   return shfl_u64(v, (K - 1) & 63);
 }
 
-__device__ __forceinline__ float lut_value(const float* lut32, const uint16_t* lut16, bool f16,
-                                           int idx) {
-  return f16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx];
-}
-
-// ADC score of one packed row: sum over m of T[m][code_m], left to right.
-template <bool F16>
-__device__ __forceinline__ float adc_row(const uint8_t* __restrict__ row, int pq_m, int ks_log2,
-                                         const float* lut32, const uint16_t* lut16) {
-  float s = 0.f;
-  int m = 0;
-  for (; m + 16 <= pq_m; m += 16) {
-    const uint4 w = *reinterpret_cast<const uint4*>(row + m);
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int b = 0; b < 16; ++b) {
-      const uint32_t code = (wv[b >> 2] >> (8 * (b & 3))) & 0xffu;
-      s = s + lut_value(lut32, lut16, F16, ((m + b) << ks_log2) + static_cast<int>(code));
-    }
-  }
-  if (m < pq_m) {
-    const uint4 w = *reinterpret_cast<const uint4*>(row + m);
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-    for (int b = 0; m + b < pq_m; ++b) {
-      const uint32_t code = (wv[b >> 2] >> (8 * (b & 3))) & 0xffu;
-      s = s + lut_value(lut32, lut16, F16, ((m + b) << ks_log2) + static_cast<int>(code));
-    }
-  }
-  return s;
+// Byte offset of (packed row pos, block b) in the tiled code layout.
+__device__ __forceinline__ int64_t code_offset(int64_t pos, int b, int nblocks) {
+  return (pos / kTile) * (static_cast<int64_t>(nblocks) * kTile * kBlock) +
+         static_cast<int64_t>(b) * (kTile * kBlock) + (pos % kTile) * kBlock;
 }
 
 struct ScanLayout {
-  size_t lut_bytes;    // table region, also reused for the final cross-wave merge
+  size_t lut_bytes;  // one block's table slice; reused for the final cross-wave merge
   size_t resid_off;
+  size_t thr_off;
   size_t bufk_off;
   size_t bufp_off;
   size_t total;
 };
 
-__host__ __device__ inline ScanLayout scan_layout(int pq_m, int ks, int dim, int f16, int kpl) {
+__host__ __device__ inline ScanLayout scan_layout(int ks, int dim, int f16, int kpl) {
   ScanLayout L;
-  const size_t table = round16(static_cast<size_t>(pq_m) * ks * (f16 ? 2u : 4u));
+  const size_t table = round16(static_cast<size_t>(kBlock) * ks * (f16 ? 2u : 4u));
   const size_t merge = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
   L.lut_bytes = table > merge ? table : merge;
   L.resid_off = L.lut_bytes;
-  L.bufk_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
+  L.thr_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
+  L.bufk_off = L.thr_off + kWaves * 8;
   L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
   L.total = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
   return L;
@@ -174,19 +163,21 @@ __host__ __device__ inline ScanLayout scan_layout(int pq_m, int ks, int dim, int
 template <int KPL, bool F16>
 __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const ScanLayout L = scan_layout(a.pq_m, a.ks, a.dim, F16 ? 1 : 0, KPL);
+  const ScanLayout L = scan_layout(a.ks, a.dim, F16 ? 1 : 0, KPL);
   float* lut32 = reinterpret_cast<float*>(smem);
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem);
   float* resid = reinterpret_cast<float*>(smem + L.resid_off);
+  uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
   const int wave = threadIdx.x >> 6, lane = lane_id();
   uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
   int32_t* bufp = reinterpret_cast<int32_t*>(smem + L.bufp_off) + wave * kBufCap;
 
   const int64_t q = blockIdx.x;
   const float* __restrict__ qv = a.queries + q * a.dim;
-  const int lut_n = a.pq_m * a.ks;
-  const int ks_log2 = __ffs(a.ks) - 1;
+  const int ks = a.ks;
+  const int ks_log2 = __ffs(ks) - 1;
   const int K = a.K;
+  const int nblocks = (a.pq_m + kBlock - 1) / kBlock;
 
   uint64_t lk[KPL];
   int32_t lp[KPL];
@@ -199,6 +190,27 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
   int cnt = 0;
   uint32_t ord_base = 0;
   unsigned long long rows_total = 0, tasks = 0;
+  if (lane == 0) wave_thr[wave] = kNoKey;
+
+  // Merges the first min(cnt, 64) buffered candidates into the wave's list and
+  // republishes the wave's threshold.
+  auto flush = [&]() {
+    const int take = cnt < 64 ? cnt : 64;
+    uint64_t bk = lane < take ? bufk[lane] : kNoKey;
+    int32_t bp = lane < take ? bufp[lane] : -1;
+    const int rest = cnt - take;
+    if (lane < rest) {
+      const uint64_t mk = bufk[64 + lane];
+      const int32_t mp = bufp[64 + lane];
+      bufk[lane] = mk;
+      bufp[lane] = mp;
+    }
+    cnt = rest;
+    sort64(bk, bp);
+    merge64<KPL>(lk, lp, bk, bp);
+    thr = kth_key<KPL>(lk, K);
+    if (lane == 0) wave_thr[wave] = thr;
+  };
 
   for (int p = 0; p < a.P; ++p) {
     const int l = a.probes[q * a.P + p];
@@ -208,72 +220,110 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
     ++tasks;
     rows_total += static_cast<unsigned long long>(rows);
 
-    __syncthreads();  // the previous list's scan no longer reads the table
+    __syncthreads();  // the previous list no longer reads resid
     const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
     for (int t = threadIdx.x; t < a.dim; t += kThreads) resid[t] = qv[t] - cv[t];
-    __syncthreads();
-    for (int e = threadIdx.x; e < lut_n; e += kThreads) {
-      const float* r = resid + (e >> ks_log2) * a.dsub;
-      const float* __restrict__ b = a.codebooks + static_cast<int64_t>(e) * a.dsub;
-      float s = 0.f;
-      for (int u = 0; u < a.dsub; ++u) {
-        const float d = r[u] - b[u];
-        s = s + d * d;
-      }
-      if (F16) {
-        lut16[e] = __half_as_ushort(__float2half_rn(s));
-      } else {
-        lut32[e] = s;
-      }
-    }
-    __syncthreads();
 
-    for (int64_t r0 = 0; r0 < rows; r0 += kThreads) {
-      const int64_t r = r0 + threadIdx.x;
-      const int64_t pos = begin + r;
-      bool valid = r < rows;
-      if (valid && a.bitset) {
-        const int64_t id = a.ids[pos];
-        valid = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
-      }
-      uint64_t key = kNoKey;
-      if (valid) {
-        const float s = adc_row<F16>(a.codes + pos * a.code_stride, a.pq_m, ks_log2, lut32, lut16);
-        key = make_key(s, ord_base + static_cast<uint32_t>(r));
-      }
-      const bool pass = key < thr;
-      const uint64_t bal = __ballot(pass);
-      if (bal) {
-        const int before = __popcll(bal & ((1ull << lane) - 1ull));
-        if (pass) {
-          bufk[cnt + before] = key;
-          bufp[cnt + before] = static_cast<int32_t>(pos);
+    for (int64_t c0 = 0; c0 < rows; c0 += kChunkRows) {
+      const int chunk = static_cast<int>(rows - c0 < kChunkRows ? rows - c0 : kChunkRows);
+      float s[kRowsPerLane];
+      uint32_t alive = 0;
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i) {
+        s[i] = 0.f;
+        const int r = static_cast<int>(threadIdx.x) + i * kThreads;
+        bool ok = r < chunk;
+        if (ok && a.bitset) {
+          const int64_t id = a.ids[begin + c0 + r];
+          ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
         }
-        cnt += __popcll(bal);
-        if (cnt >= 64) {
-          uint64_t bk = bufk[lane];
-          int32_t bp = bufp[lane];
-          const int rest = cnt - 64;
-          if (lane < rest) {
-            const uint64_t mk = bufk[64 + lane];
-            const int32_t mp = bufp[64 + lane];
-            bufk[lane] = mk;
-            bufp[lane] = mp;
+        alive |= static_cast<uint32_t>(ok) << i;
+      }
+
+      for (int b = 0; b < nblocks; ++b) {
+        // Also the barrier that retires the previous block's table slice (and
+        // publishes resid for the first block).
+        if (!__syncthreads_or(alive != 0)) break;
+        const int mb = a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock;
+        const int slice = mb << ks_log2;
+        for (int e = threadIdx.x; e < slice; e += kThreads) {
+          const int m = b * kBlock + (e >> ks_log2);
+          const float* r = resid + m * a.dsub;
+          const float* __restrict__ cw =
+              a.codebooks + (static_cast<int64_t>(m) * ks + (e & (ks - 1))) * a.dsub;
+          float acc = 0.f;
+          for (int u = 0; u < a.dsub; ++u) {
+            const float d = r[u] - cw[u];
+            acc = acc + d * d;
           }
-          cnt = rest;
-          sort64(bk, bp);
-          merge64<KPL>(lk, lp, bk, bp);
-          thr = kth_key<KPL>(lk, K);
+          if (F16) {
+            lut16[e] = __half_as_ushort(__float2half_rn(acc));
+          } else {
+            lut32[e] = acc;
+          }
+        }
+        __syncthreads();
+        uint32_t thr_hi = 0xffffffffu;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const uint32_t h = static_cast<uint32_t>(wave_thr[w] >> 32);
+          thr_hi = h < thr_hi ? h : thr_hi;
+        }
+        // Rows i and i+1 of a lane are kThreads = 4 tiles apart: one base
+        // address plus a uniform stride reaches all of them.
+        const uint8_t* __restrict__ row0 =
+            a.codes + code_offset(begin + c0 + threadIdx.x, b, nblocks);
+        const int64_t row_step = static_cast<int64_t>(kThreads / kTile) * nblocks * kTile * kBlock;
+#pragma unroll
+        for (int i = 0; i < kRowsPerLane; ++i) {
+          if (!((alive >> i) & 1u)) continue;
+          const uint2 w = *reinterpret_cast<const uint2*>(row0 + i * row_step);
+          const uint32_t wv[2] = {w.x, w.y};
+          float acc = s[i];
+          if (mb == kBlock) {
+#pragma unroll
+            for (int j = 0; j < kBlock; ++j) {
+              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+              const int idx = (j << ks_log2) + code;
+              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
+            }
+          } else {
+            for (int j = 0; j < mb; ++j) {
+              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+              const int idx = (j << ks_log2) + code;
+              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
+            }
+          }
+          s[i] = acc;
+          if (score_key(acc) > thr_hi) alive &= ~(1u << i);
         }
       }
+
+      // Rows still alive carry their complete score: offer them to the wave's list.
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i) {
+        if (i * kThreads >= chunk) break;
+        const int r = static_cast<int>(threadIdx.x) + i * kThreads;
+        const bool ok = ((alive >> i) & 1u) != 0;
+        const uint64_t key =
+            ok ? make_key(s[i], ord_base + static_cast<uint32_t>(c0) + static_cast<uint32_t>(r))
+               : kNoKey;
+        const bool pass = key < thr;
+        const uint64_t bal = __ballot(pass);
+        if (bal) {
+          const int before = __popcll(bal & ((1ull << lane) - 1ull));
+          if (pass) {
+            bufk[cnt + before] = key;
+            bufp[cnt + before] = static_cast<int32_t>(begin + c0 + r);
+          }
+          cnt += __popcll(bal);
+          if (cnt >= 64) flush();
+        }
+      }
+      // Fold what is left so the threshold used for pruning stays current.
+      if (cnt > 0) flush();
     }
     ord_base += static_cast<uint32_t>(rows);
-  }
-  if (cnt > 0) {
-    uint64_t bk = lane < cnt ? bufk[lane] : kNoKey;
-    int32_t bp = lane < cnt ? bufp[lane] : -1;
-    sort64(bk, bp);
-    merge64<KPL>(lk, lp, bk, bp);
   }
 
   // Cross-wave merge: each wave publishes its sorted list, wave 0 folds in the rest.
@@ -341,7 +391,7 @@ int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512
 extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
                                           int32_t lut_f16, int32_t K) {
   if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE) return 0;
-  const size_t b = scan_layout(pq_m, ks, dim, lut_f16 ? 1 : 0, kpl_for(K)).total;
+  const size_t b = scan_layout(ks, dim, lut_f16 ? 1 : 0, kpl_for(K)).total;
   return b <= 160u * 1024u ? b : 0;
 }
 
@@ -352,11 +402,11 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
       !a.ids || !a.out_keys || !a.out_pos || !a.out_count || !a.counters || a.nq > 0x7fffffff ||
       a.dim <= 0 || a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 ||
-      (a.ks & (a.ks - 1)) != 0 || a.code_stride < a.pq_m || (a.code_stride & 15) != 0 ||
+      (a.ks & (a.ks - 1)) != 0 || a.code_blocks != (a.pq_m + kBlock - 1) / kBlock ||
       static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
     return hipErrorInvalidValue;
   const int kpl = kpl_for(a.K);
-  const size_t lds = scan_layout(a.pq_m, a.ks, a.dim, a.lut_f16 ? 1 : 0, kpl).total;
+  const size_t lds = scan_layout(a.ks, a.dim, a.lut_f16 ? 1 : 0, kpl).total;
   if (lds > 160u * 1024u) return hipErrorInvalidValue;
   if (a.lut_f16) {
     switch (kpl) {
