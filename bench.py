@@ -67,6 +67,18 @@ def exact_topk(base_t, q_t, k, torch):
     return best_i.cpu().numpy()
 
 
+def profiled_traffic(config_name):
+    """HBM bytes per k_scan launch from the committed rocprofv3 summary of this
+    workload (FETCH_SIZE and WRITE_SIZE passes, scaled by known-size copies)."""
+    path = ROOT / "profiles" / f"k_scan_{config_name}.md"
+    if not path.exists():
+        return None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1]), str(path.relative_to(ROOT))
+    return None, None
+
+
 def recall(got, truth):
     hits = 0
     for g, t in zip(got, truth):
@@ -137,6 +149,10 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="run one device-to-device copy and one elementwise copy of this many "
+                         "MiB before the timed steps (known-size kernels that scale rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -183,6 +199,16 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     log(f"{args.warmup} warmup steps done")
+    if args.calibrate_copy_mb > 0:
+        count = args.calibrate_copy_mb * (1 << 20) // 4
+        src = torch.ones(count, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)                     # device-to-device copy kernel
+        torch.mul(src, 2.0, out=dst)       # elementwise kernel: reads and writes count*4 bytes
+        torch.cuda.synchronize()
+        log(f"calibration copies of {args.calibrate_copy_mb} MiB done")
+        del src, dst
     s0 = res.ivfpq_search_stats()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -204,6 +230,7 @@ def main() -> int:
                 for name in ("coarse_pairwise", "coarse_topk", "adc_scan_select",
                              "refine_distance", "total_wall")}
 
+    traffic, traffic_src = profiled_traffic(cfg.name)
     gpu_ids = did.cpu().numpy()
     gpu_d = dd.cpu().numpy()
 
@@ -255,7 +282,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "kernel": "k_scan (fused LUT build + code scan + shortlist)",
             "algorithmic_bytes_per_launch": code_bytes,
             "avg_launch_ms": scan_s * 1e3,
