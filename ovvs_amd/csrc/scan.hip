@@ -132,6 +132,82 @@ __device__ __forceinline__ uint64_t kth_key(const uint64_t (&lk)[KPL], int K) {
   return shfl_u64(v, (K - 1) & 63);
 }
 
+// Inserts one key (wave-uniform) into the sorted list, dropping the largest.
+template <int KPL>
+__device__ __forceinline__ void insert_one(uint64_t (&lk)[KPL], int32_t (&lp)[KPL], uint64_t key,
+                                           int32_t pos) {
+  const int lane = lane_id();
+  int at = 0;  // number of list elements smaller than key
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) at += __popcll(__ballot(lk[j] < key));
+  uint64_t prev_tail = 0;
+  int32_t prev_tail_p = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    // Element e = j*64 + lane takes element e-1 when e > at.
+    uint64_t up = shfl_u64(lk[j], (lane + 63) & 63);
+    int32_t upp = __shfl(lp[j], (lane + 63) & 63, 64);
+    const uint64_t tail = shfl_u64(lk[j], 63);
+    const int32_t tailp = __shfl(lp[j], 63, 64);
+    if (lane == 0) {
+      up = prev_tail;
+      upp = prev_tail_p;
+    }
+    const int e = j * 64 + lane;
+    if (e == at) {
+      lk[j] = key;
+      lp[j] = pos;
+    } else if (e > at) {
+      lk[j] = up;
+      lp[j] = upp;
+    }
+    prev_tail = tail;
+    prev_tail_p = tailp;
+  }
+}
+
+// Score whose keys are above `key`'s score word: the float the order-preserving
+// transform maps to key >> 32 (+inf for an empty slot, NaN stays NaN).
+__device__ __forceinline__ float key_score(uint64_t key) {
+  const uint32_t k = static_cast<uint32_t>(key >> 32);
+  if (k == 0xffffffffu) return __builtin_inff();
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// Builds the table slice of subspaces [m0, m0 + mb) into LDS: entry
+// (m - m0) * ks + j = sum_u (r[m*dsub+u] - B[m][j][u])^2, left to right from +0.
+template <int DSUB, bool F16>
+__device__ __forceinline__ void build_slice(const float* resid, const float* __restrict__ codebooks,
+                                            int m0, int mb, int ks, int ks_log2, int dsub,
+                                            float* lut32, uint16_t* lut16) {
+  const int d = DSUB > 0 ? DSUB : dsub;
+  const int slice = mb << ks_log2;
+  for (int e = threadIdx.x; e < slice; e += 256) {
+    const int m = m0 + (e >> ks_log2);
+    const float* r = resid + m * d;
+    const float* __restrict__ cw = codebooks + (static_cast<int64_t>(m) * ks + (e & (ks - 1))) * d;
+    float acc = 0.f;
+    if (DSUB > 0) {
+#pragma unroll
+      for (int u = 0; u < DSUB; ++u) {
+        const float t = r[u] - cw[u];
+        acc = acc + t * t;
+      }
+    } else {
+      for (int u = 0; u < d; ++u) {
+        const float t = r[u] - cw[u];
+        acc = acc + t * t;
+      }
+    }
+    if (F16) {
+      lut16[e] = __half_as_ushort(__float2half_rn(acc));
+    } else {
+      lut32[e] = acc;
+    }
+  }
+}
+
 // Byte offset of (packed row pos, block b) in the tiled code layout.
 __device__ __forceinline__ int64_t code_offset(int64_t pos, int b, int nblocks) {
   return (pos / kTile) * (static_cast<int64_t>(nblocks) * kTile * kBlock) +
@@ -161,8 +237,7 @@ __host__ __device__ inline ScanLayout scan_layout(int ks, int dim, int f16, int 
 }
 
 template <int KPL, bool F16>
-__global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char* smem) {
   const ScanLayout L = scan_layout(a.ks, a.dim, F16 ? 1 : 0, KPL);
   float* lut32 = reinterpret_cast<float*>(smem);
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem);
@@ -245,30 +320,31 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
         // publishes resid for the first block).
         if (!__syncthreads_or(alive != 0)) break;
         const int mb = a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock;
-        const int slice = mb << ks_log2;
-        for (int e = threadIdx.x; e < slice; e += kThreads) {
-          const int m = b * kBlock + (e >> ks_log2);
-          const float* r = resid + m * a.dsub;
-          const float* __restrict__ cw =
-              a.codebooks + (static_cast<int64_t>(m) * ks + (e & (ks - 1))) * a.dsub;
-          float acc = 0.f;
-          for (int u = 0; u < a.dsub; ++u) {
-            const float d = r[u] - cw[u];
-            acc = acc + d * d;
-          }
-          if (F16) {
-            lut16[e] = __half_as_ushort(__float2half_rn(acc));
-          } else {
-            lut32[e] = acc;
-          }
+        switch (a.dsub) {
+          case 1:
+            build_slice<1, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 1, lut32, lut16);
+            break;
+          case 2:
+            build_slice<2, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 2, lut32, lut16);
+            break;
+          case 4:
+            build_slice<4, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 4, lut32, lut16);
+            break;
+          case 8:
+            build_slice<8, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 8, lut32, lut16);
+            break;
+          default:
+            build_slice<0, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, a.dsub, lut32,
+                                lut16);
         }
         __syncthreads();
-        uint32_t thr_hi = 0xffffffffu;
+        // Prune bound: the smallest K-th key any wave has published. Partial
+        // sums are >= +0 (or NaN, never pruned), so comparing floats against the
+        // decoded score is the same as comparing order-preserving keys.
+        uint64_t tmin = wave_thr[0];
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const uint32_t h = static_cast<uint32_t>(wave_thr[w] >> 32);
-          thr_hi = h < thr_hi ? h : thr_hi;
-        }
+        for (int w = 1; w < kWaves; ++w) tmin = wave_thr[w] < tmin ? wave_thr[w] : tmin;
+        const float thr_f = key_score(tmin);
         // Rows i and i+1 of a lane are kThreads = 4 tiles apart: one base
         // address plus a uniform stride reaches all of them.
         const uint8_t* __restrict__ row0 =
@@ -295,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
             }
           }
           s[i] = acc;
-          if (score_key(acc) > thr_hi) alive &= ~(1u << i);
+          if (acc > thr_f) alive &= ~(1u << i);
         }
       }
 
@@ -303,6 +379,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
 #pragma unroll
       for (int i = 0; i < kRowsPerLane; ++i) {
         if (i * kThreads >= chunk) break;
+        if (__ballot((alive >> i) & 1u) == 0) continue;
         const int r = static_cast<int>(threadIdx.x) + i * kThreads;
         const bool ok = ((alive >> i) & 1u) != 0;
         const uint64_t key =
@@ -320,8 +397,16 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
           if (cnt >= 64) flush();
         }
       }
-      // Fold what is left so the threshold used for pruning stays current.
-      if (cnt > 0) flush();
+      // Fold what is left so the threshold used for pruning stays current: a few
+      // keys are inserted one by one, more go through the sort-and-merge.
+      if (cnt > 0 && cnt <= 8) {
+        for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
+        cnt = 0;
+        thr = kth_key<KPL>(lk, K);
+        if (lane == 0) wave_thr[wave] = thr;
+      } else if (cnt > 0) {
+        flush();
+      }
     }
     ord_base += static_cast<uint32_t>(rows);
   }
@@ -371,9 +456,29 @@ __global__ __launch_bounds__(kThreads) void k_scan(const OvvsScanArgs a) {
   }
 }
 
+// Shortlists of up to 128 keys fit 5 waves per SIMD without spilling; longer
+// register lists keep the compiler's own allocation.
+template <int KPL, bool F16>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void k_scan(
+    const OvvsScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  scan_query<KPL, F16>(a, smem);
+}
+
+template <int KPL, bool F16>
+__global__ __launch_bounds__(kThreads) void k_scan_long(const OvvsScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  scan_query<KPL, F16>(a, smem);
+}
+
 template <int KPL, bool F16>
 hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
-  auto fn = k_scan<KPL, F16>;
+  void (*fn)(OvvsScanArgs);
+  if constexpr (KPL <= 2) {
+    fn = k_scan<KPL, F16>;
+  } else {
+    fn = k_scan_long<KPL, F16>;
+  }
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
