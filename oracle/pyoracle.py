@@ -45,6 +45,24 @@ class Ipq1:
     assign: np.ndarray      # [n] i32
     lists: list             # nlist arrays of i64 ids
 
+    def to_bytes(self) -> bytes:
+        """The IPQ1 v1 file of this index (the inverse of read_ipq1), used by tests to
+        write indexes with hand-made centroids."""
+        head = np.array([0x31515049, 1], dtype=np.uint32).tobytes()
+        head += np.array([self.n, self.dim], dtype=np.int64).tobytes()
+        head += np.array([self.nlist, self.pq_m, self.pq_ks, self.dsub, self.metric],
+                         dtype=np.int32).tobytes()
+        parts = [head,
+                 np.ascontiguousarray(self.centroids, dtype=np.float32).tobytes(),
+                 np.ascontiguousarray(self.codebooks, dtype=np.float32).tobytes(),
+                 np.ascontiguousarray(self.codes, dtype=np.uint8).tobytes(),
+                 np.ascontiguousarray(self.dataset, dtype=np.float32).tobytes(),
+                 np.ascontiguousarray(self.assign, dtype=np.int32).tobytes()]
+        for l in self.lists:
+            parts.append(np.int32(len(l)).tobytes())
+            parts.append(np.ascontiguousarray(l, dtype=np.int64).tobytes())
+        return b"".join(parts)
+
     def packed(self):
         """List-major (packed_codes [n, pq_m], packed_ids [n], offsets [nlist+1])."""
         ids = np.concatenate([np.asarray(l, dtype=np.int64) for l in self.lists]) \

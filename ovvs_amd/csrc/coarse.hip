@@ -200,12 +200,14 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
 
 __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S, int64_t ldS,
                                                      int N, int P, int M,
+                                                     const int32_t* __restrict__ flags,
                                                      int32_t* __restrict__ out) {
   extern __shared__ uint64_t sel[];  // [M]
   __shared__ uint32_t hist[256];
   __shared__ uint32_t scan_scratch[4];
   __shared__ uint32_t s_digit, s_need;
   const int64_t row = blockIdx.x;
+  if (flags && flags[row] == 0) return;  // uniform over the workgroup
   const float* r = S + row * ldS;
 
   // 1. Radix select of the P-th smallest 32-bit score key.
@@ -311,8 +313,9 @@ extern "C" hipError_t ovvs_hip_coarse_argmin(const float* Q, const float* qn, in
   return hipGetLastError();
 }
 
-extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N,
-                                           int32_t P, int32_t* out, hipStream_t stream) {
+extern "C" hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nrows,
+                                                   int32_t N, int32_t P, const int32_t* flags,
+                                                   int32_t* out, hipStream_t stream) {
   if (nrows <= 0) return hipSuccess;
   if (!S || !out || N <= 0 || P <= 0 || P > N || P > OVVS_HIP_MAX_PROBES || ldS < N ||
       nrows > 0x7fffffff)
@@ -320,6 +323,11 @@ extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t 
   int M = 1;
   while (M < P) M <<= 1;
   hipLaunchKernelGGL(k_select_topk, dim3(static_cast<uint32_t>(nrows)), dim3(256),
-                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, out);
+                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, flags, out);
   return hipGetLastError();
+}
+
+extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N,
+                                           int32_t P, int32_t* out, hipStream_t stream) {
+  return ovvs_hip_select_topk_flagged(S, ldS, nrows, N, P, nullptr, out, stream);
 }

@@ -312,7 +312,19 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
   OVVS_HIP_TRY(ovvs_hip_row_norms(d->dataset.as<float>(), n, static_cast<int32_t>(dim),
                                   d->xnorm.as<float>(), s));
   work.kernel_launches += 2;
+  std::vector<float> cmfma(ovvs_hip_probe_cmfma_floats(static_cast<int32_t>(dim), nlist));
+  if (!cmfma.empty()) {
+    ovvs_probe_pack_cmfma(centroids.data(), nlist, static_cast<int32_t>(dim), cmfma.data());
+    OVVS_TRY(alloc(d->cmfma, cmfma.size() * 4, work));
+    OVVS_TRY(h2d(d->cmfma.get(), cmfma.data(), cmfma.size() * 4, s, work));
+  }
+  std::vector<float> cnorm(static_cast<size_t>(nlist));
+  OVVS_TRY(d2h(cnorm.data(), d->cnorm.get(), cnorm.size() * 4, s, work));
   OVVS_TRY(sync(s, work));
+  for (const float v : cnorm) {
+    if (!(v <= d->cnorm_max)) d->cnorm_max = std::isfinite(v) ? v : INFINITY;
+    if (std::isinf(d->cnorm_max)) break;
+  }
   dev = std::move(d);
   return OVVS_STATUS_SUCCESS;
 }

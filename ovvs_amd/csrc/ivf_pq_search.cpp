@@ -134,6 +134,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     need += device_io ? 0 : align256(static_cast<size_t>(nq) * dim * 4);  // queries
     need += align256(static_cast<size_t>(nq) * 4);                        // query norms
     need += align256(static_cast<size_t>(nq) * P * 4);                    // probes
+    need += align256(static_cast<size_t>(nq) * 4);                        // probe fallback flags
     need += align256(static_cast<size_t>(qc) * ix.nlist * 4);             // score chunk
     need += align256(static_cast<size_t>(nq) * R * 8);                    // shortlist keys
     need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
@@ -150,6 +151,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     if (!device_io) d_q = cv.take<float>(static_cast<size_t>(nq) * dim);
     float* d_qn = cv.take<float>(static_cast<size_t>(nq));
     int32_t* d_probes = cv.take<int32_t>(static_cast<size_t>(nq) * P);
+    int32_t* d_flags = cv.take<int32_t>(static_cast<size_t>(nq));
     float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
     uint64_t* d_skeys = cv.take<uint64_t>(static_cast<size_t>(nq) * R);
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
@@ -177,14 +179,46 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     SEARCH_HIP(hipEventRecord(ev[0], s));
     SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
     int64_t chunks = 0;
-    for (int64_t q0 = 0; q0 < nq; q0 += qc) {
-      const int64_t cnt = std::min(qc, nq - q0);
-      SEARCH_HIP(ovvs_hip_coarse_scores(d_q + q0 * dim, d_qn + q0, cnt, dv.centroids.as<float>(),
-                                        dv.cnorm.as<float>(), ix.nlist, dim, d_scores, ix.nlist,
-                                        s));
-      if (q0 == 0) SEARCH_HIP(hipEventRecord(ev[1], s));
-      SEARCH_HIP(ovvs_hip_select_topk(d_scores, ix.nlist, cnt, ix.nlist, P, d_probes + q0 * P, s));
-      ++chunks;
+    const bool mfma_probe =
+        dv.cmfma.get() != nullptr && ovvs_hip_probe_mfma_supported(dim, ix.nlist, P) != 0;
+    if (mfma_probe) {
+      // Matrix-core probe with exact re-score; flagged queries take the exact route.
+      OvvsProbeArgs pa{};
+      pa.queries = d_q;
+      pa.qnorm = d_qn;
+      pa.nq = nq;
+      pa.dim = dim;
+      pa.nlist = ix.nlist;
+      pa.P = P;
+      pa.centroids = dv.centroids.as<float>();
+      pa.cmfma = dv.cmfma.as<float>();
+      pa.cnorm = dv.cnorm.as<float>();
+      pa.cnorm_max = dv.cnorm_max;
+      pa.probes = d_probes;
+      pa.fallback = d_flags;
+      SEARCH_HIP(ovvs_hip_probe_mfma(&pa, s));
+      SEARCH_HIP(hipEventRecord(ev[1], s));
+      for (int64_t q0 = 0; q0 < nq; q0 += qc) {
+        const int64_t cnt = std::min(qc, nq - q0);
+        SEARCH_HIP(ovvs_hip_probe_exact_rows(d_q + q0 * dim, d_qn + q0, cnt,
+                                             dv.centroids.as<float>(), dv.cnorm.as<float>(),
+                                             ix.nlist, dim, d_flags + q0, d_scores, s));
+        SEARCH_HIP(ovvs_hip_select_topk_flagged(d_scores, ix.nlist, cnt, ix.nlist, P,
+                                                d_flags + q0, d_probes + q0 * P, s));
+        ++chunks;
+      }
+      work.kernel_launches += 1;
+    } else {
+      for (int64_t q0 = 0; q0 < nq; q0 += qc) {
+        const int64_t cnt = std::min(qc, nq - q0);
+        SEARCH_HIP(ovvs_hip_coarse_scores(d_q + q0 * dim, d_qn + q0, cnt,
+                                          dv.centroids.as<float>(), dv.cnorm.as<float>(),
+                                          ix.nlist, dim, d_scores, ix.nlist, s));
+        if (q0 == 0) SEARCH_HIP(hipEventRecord(ev[1], s));
+        SEARCH_HIP(
+            ovvs_hip_select_topk(d_scores, ix.nlist, cnt, ix.nlist, P, d_probes + q0 * P, s));
+        ++chunks;
+      }
     }
     SEARCH_HIP(hipEventRecord(ev[2], s));
 

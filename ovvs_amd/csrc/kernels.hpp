@@ -43,6 +43,52 @@ hipError_t ovvs_hip_coarse_scores(const float* Q, const float* qn, int64_t nq, c
 // out[row*P + r] (reference cpu_prims.cpp:24-106). P <= OVVS_HIP_MAX_PROBES, P <= N.
 hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N, int32_t P,
                                 int32_t* out, hipStream_t stream);
+// The same for the rows with flags[row] != 0 only; other rows are left untouched.
+hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nrows, int32_t N,
+                                        int32_t P, const int32_t* flags, int32_t* out,
+                                        hipStream_t stream);
+
+// ---- coarse probe on the fp32 matrix cores (probe.hip) ----
+
+// Limits of the fused probe: dim <= 16 * OVVS_PROBE_MAX_DS4 (query fragments held in
+// registers), P <= OVVS_PROBE_MAX_P, at least 2P of its (at most OVVS_PROBE_MAX_GROUPS)
+// centroid groups, at most 256 (P <= 64) or OVVS_PROBE_CAP exact re-scores per query
+// (a query with more takes the exact route).
+#define OVVS_PROBE_MAX_DS4 8
+#define OVVS_PROBE_MAX_P 256
+#define OVVS_PROBE_MAX_GROUPS 512
+#define OVVS_PROBE_CAP 512
+
+struct OvvsProbeArgs {
+  const float* queries;    // [nq * dim]
+  const float* qnorm;      // [nq], exact row norms
+  int64_t nq;
+  int32_t dim;
+  int32_t nlist;
+  int32_t P;               // probes per query
+  const float* centroids;  // [nlist * dim] row-major (exact re-score)
+  const float* cmfma;      // centroids in matrix-core operand order, see
+                           // ovvs_probe_pack_cmfma
+  const float* cnorm;      // [nlist], exact row norms
+  float cnorm_max;         // max of cnorm (+inf if any is NaN or inf)
+  int32_t* probes;         // [nq * P] out, rank order (rows with fallback[q] = 0)
+  int32_t* fallback;       // [nq] out: 1 where the query needs the exact route
+};
+
+// 1 when the fused probe handles these shapes.
+int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t P);
+// Floats in the operand-ordered centroid copy (0 if dim is unsupported).
+size_t ovvs_hip_probe_cmfma_floats(int32_t dim, int32_t nlist);
+// Host-side packing of that copy: for tile t (16 centroids), step group s4 (16
+// dims) and lane l, the float4 at ((t * ceil(dim/16) + s4) * 64 + l) holds, for
+// e = 0..3, C[16t + l%16][16*s4 + 4e + l/16] (zero past nlist or dim).
+void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, float* out);
+// Probe selection for every query; flags the queries the exact route must finish.
+hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream);
+// Exact coarse scores S[q*nlist + c] of every centroid, for flagged queries only.
+hipError_t ovvs_hip_probe_exact_rows(const float* Q, const float* qn, int64_t nq, const float* C,
+                                     const float* cn, int32_t nlist, int32_t dim,
+                                     const int32_t* flags, float* S, hipStream_t stream);
 
 // Exact argmin over all centroids for each row of Q (top-1 of the coarse score
 // under the same total order), fused with the score computation: labels[i].

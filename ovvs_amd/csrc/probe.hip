@@ -1,0 +1,420 @@
+// probe.hip — coarse probe on the fp32 matrix cores with fused candidate selection,
+// exact re-score and an exact fallback, for IVF-PQ search on gfx950.
+//
+// The probe set of query q is the first P centroids under the total order on
+// (s(q,c), c) with the exact fp32 score s = (|q|^2 + |c|^2) - 2*(q.c), each term a
+// left-to-right sum (reference src/neighbors/indexes.cpp:597-606,
+// src/prim/mixer.cpp:174-199, src/prim/cpu/cpu_prims.cpp:24-106).
+//
+// k_probe_mfma, one workgroup of kWaves wave64s per 16 queries:
+//   pass 1   v_mfma_f32_16x16x4f32 tiles of 16 queries x 16 centroids give approximate
+//            scores a(q,c). The tiles are cut into nch chunks of gt consecutive tiles;
+//            group (chunk, column j) holds the centroids 16t + j of the chunk's tiles,
+//            and each lane keeps the running minimum of a over its group in registers.
+//            v_q is the P-th smallest of the 16 * nch group minima (as order keys): at
+//            least P distinct centroids (one per group) have a <= t_q, the score v_q
+//            encodes.
+//   bound    E_q >= |a(q,c) - s(q,c)| for every centroid c: both dot products are
+//            fp32 sums of dim products, so each is within gamma_n * |q| * |c|_max of
+//            the real dot product (n = dim + 4, unit roundoff 2^-23 to allow any
+//            rounding mode of the matrix core, plus an absolute term for flushed
+//            subnormals), and the shared |q|^2 + |c|^2 term is rounded once more.
+//   pass 2   every centroid with !(a > T_q), T_q = t_q + 2 E_q rounded up, is a
+//            candidate. A centroid outside has s > t_q + E_q >= s of at least P
+//            candidates, so P entries precede it in the exact order: the exact first
+//            P are all candidates.
+//   pass 3   each candidate is re-scored with the reference's sequential fp32 sums;
+//            its rank is the number of candidates with a smaller (s, c) key, and the
+//            P of rank < P are the probes in order, bit for bit.
+// A query with more candidates than the re-score capacity, or fewer than P (only NaN
+// or infinite inputs can cause that), is flagged in `fallback`; k_probe_exact_rows and
+// the flagged row selection of coarse.hip then rank it from exact scores of every
+// centroid.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+using namespace ovvs_dev;
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 16;                     // queries per workgroup (MFMA M dimension)
+constexpr int kRowsPerWave = kRows / kWaves;  // rows each wave selects and ranks
+constexpr int kMaxChunks = OVVS_PROBE_MAX_GROUPS / 16;
+
+// Launch shape and LDS carve of one probe launch.
+struct ProbeShape {
+  int ntile;   // 16-centroid tiles (nlist padded to 16)
+  int gt;      // tiles per chunk
+  int nch;     // chunks; 16 * nch group slots
+  int cap;     // re-score capacity per query
+  int dq;      // LDS row stride of the staged queries (dim rounded up to 4)
+  int real_groups;  // groups holding at least one real centroid
+  size_t lds;  // dynamic LDS bytes
+};
+
+constexpr size_t align16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
+
+// LDS: qs [16][dq] f32 | count [16] i32 | thr [16] f32 | area: gmin [16][16*nch] u32
+// during passes 1-2, then slot [16][cap] u64 (candidate id, later its exact key).
+struct Carve {
+  float* qs;
+  int32_t* count;
+  float* thr;
+  uint32_t* gmin;
+  uint64_t* slot;
+};
+
+__device__ __forceinline__ Carve carve(unsigned char* base, const ProbeShape& sh) {
+  Carve c;
+  c.qs = reinterpret_cast<float*>(base);
+  unsigned char* p = base + align16(static_cast<size_t>(kRows) * sh.dq * 4);
+  c.count = reinterpret_cast<int32_t*>(p);
+  c.thr = reinterpret_cast<float*>(p + kRows * 4);
+  p += align16(2 * kRows * 4);
+  c.gmin = reinterpret_cast<uint32_t*>(p);
+  c.slot = reinterpret_cast<uint64_t*>(p);
+  return c;
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Approximate dot products of tile t: lane holds rows 4*(lane/16)+r, column lane%16.
+// The A operand a[s] = Q[row lane%16][4s + lane/16]; the centroid operand comes from
+// the operand-ordered copy (OvvsProbeArgs::cmfma).
+template <int DS4>
+__device__ __forceinline__ f32x4 tile_dot(const float (&a)[4 * DS4],
+                                          const float* __restrict__ cm, int t) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const float4* src =
+      reinterpret_cast<const float4*>(cm) + static_cast<int64_t>(t) * DS4 * 64 + lane_id();
+  float4 b[DS4];
+#pragma unroll
+  for (int s4 = 0; s4 < DS4; ++s4) b[s4] = src[s4 * 64];
+#pragma unroll
+  for (int s4 = 0; s4 < DS4; ++s4) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 0], b[s4].x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 1], b[s4].y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 2], b[s4].z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 3], b[s4].w, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// seq_dot(q, c, dim) with q in LDS and c in global memory, read 16 bytes at a time
+// when dim % 4 == 0 (rows then 16-byte aligned); the same left-to-right sum.
+__device__ __forceinline__ float exact_dot(const float* __restrict__ q,
+                                           const float* __restrict__ c, int dim) {
+  if ((dim & 3) != 0) return seq_dot(q, c, dim);
+  const float4* c4 = reinterpret_cast<const float4*>(c);
+  const float4* q4 = reinterpret_cast<const float4*>(q);
+  float s = 0.f;
+  int i = 0;
+  for (; i + 4 <= dim / 4; i += 4) {
+    float4 v[4], w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = c4[i + j];
+      w[j] = q4[i + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s = s + w[j].x * v[j].x;
+      s = s + w[j].y * v[j].y;
+      s = s + w[j].z * v[j].z;
+      s = s + w[j].w * v[j].w;
+    }
+  }
+  for (; i < dim / 4; ++i) {
+    const float4 v = c4[i], w = q4[i];
+    s = s + w.x * v.x;
+    s = s + w.y * v.y;
+    s = s + w.z * v.z;
+    s = s + w.w * v.w;
+  }
+  return s;
+}
+
+// Score of a 32-bit order key (the inverse of score_key); the NaN key gives +inf.
+__device__ __forceinline__ float key_to_score(uint32_t k) {
+  if (k == 0xffffffffu) return __builtin_inff();
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// The next float above a finite f.
+__device__ __forceinline__ float next_up(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) == 0) return __uint_as_float(1u);
+  return __uint_as_float((u & 0x80000000u) ? u - 1u : u + 1u);
+}
+
+// Candidate bound T = t + 2E for one query (see the file comment), rounded up.
+__device__ float candidate_bound(float t, float qn, float cn_max, int dim) {
+  if (!(t < __builtin_inff()) || !(qn < __builtin_inff()) || !(cn_max < __builtin_inff()))
+    return __builtin_inff();
+  const double u = 1.1920928955078125e-7;  // 2^-23
+  const double n = static_cast<double>(dim) + 4.0;
+  const double gamma = n * u / (1.0 - n * u);
+  const double qd = static_cast<double>(qn) * (1.0 + 4.0 * n * u);
+  const double cd = static_cast<double>(cn_max) * (1.0 + 4.0 * n * u);
+  const double S = sqrt(qd * cd) * (1.0 + 1e-6);
+  const double E = 2.0 * (4.0 * gamma * S + 2.0 * u * (qd + cd + 2.0 * S)) + n * 1e-30;
+  const double T = static_cast<double>(t) + 2.0 * E;
+  float f = static_cast<float>(T);
+  if (static_cast<double>(f) < T && f < __builtin_inff()) f = next_up(f);
+  return f;
+}
+
+template <int DS4>
+__global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
+                                                         const ProbeShape shape) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const Carve L = carve(smem, shape);
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int dim = p.dim, dq = shape.dq;
+
+  // Stage the 16 query rows (zero past dim and past nq).
+  for (int i = static_cast<int>(threadIdx.x); i < kRows * dq; i += kThreads) {
+    const int r = i / dq, t = i - r * dq;
+    const int64_t q = q0 + r;
+    L.qs[i] = (q < p.nq && t < dim) ? p.queries[q * dim + t] : 0.f;
+  }
+  if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
+  __syncthreads();
+
+  float a[4 * DS4];
+#pragma unroll
+  for (int s = 0; s < 4 * DS4; ++s) {
+    const int k = 4 * s + (lane >> 4);
+    a[s] = k < dim ? L.qs[(lane & 15) * dq + k] : 0.f;
+  }
+  float qn[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = q0 + 4 * (lane >> 4) + r;
+    qn[r] = row < p.nq ? p.qnorm[row] : 0.f;
+  }
+  const int col = lane & 15;
+
+  // Pass 1: running minimum of a over each (chunk, column) group.
+  for (int ch = wave; ch < shape.nch; ch += kWaves) {
+    const int t0 = ch * shape.gt;
+    const int t1 = min(t0 + shape.gt, shape.ntile);
+    float m[4] = {__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff()};
+    for (int t = t0; t < t1; ++t) {
+      const f32x4 acc = tile_dot<DS4>(a, p.cmfma, t);
+      const int c = 16 * t + col;
+      if (c < p.nlist) {
+        const float cn = p.cnorm[c];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m[r] = __builtin_fminf(m[r], (qn[r] + cn) - 2.f * acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      L.gmin[(4 * (lane >> 4) + r) * (16 * shape.nch) + ch * 16 + col] = score_key(m[r]);
+  }
+  __syncthreads();
+
+  // The P-th smallest group minimum of each row, bit by bit from the top: v is the
+  // smallest key with at least P group minima <= v. Each lane holds its slots.
+  const int ng = 16 * shape.nch;
+  for (int rr = 0; rr < kRowsPerWave; ++rr) {
+    const int row = kRowsPerWave * wave + rr;
+    uint32_t g[kMaxChunks / 4];
+#pragma unroll
+    for (int i = 0; i < kMaxChunks / 4; ++i) {
+      const int s = lane + 64 * i;
+      g[i] = s < ng ? L.gmin[row * ng + s] : 0xffffffffu;
+    }
+    uint32_t v = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t probe = v | ((1u << b) - 1u);
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < kMaxChunks / 4; ++i) cnt += __popcll(__ballot(g[i] <= probe));
+      if (cnt < p.P) v |= 1u << b;
+    }
+    if (lane == 0) {
+      const int64_t q = q0 + row;
+      const float qnr = q < p.nq ? p.qnorm[q] : 0.f;
+      L.thr[row] = candidate_bound(key_to_score(v), qnr, p.cnorm_max, dim);
+    }
+  }
+  __syncthreads();
+
+  // Pass 2: every centroid whose approximate score is not above the bound.
+  float T[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) T[r] = L.thr[4 * (lane >> 4) + r];
+  const int cap = shape.cap;
+  for (int t = wave; t < shape.ntile; t += kWaves) {
+    const f32x4 acc = tile_dot<DS4>(a, p.cmfma, t);
+    const int c = 16 * t + col;
+    if (c < p.nlist) {
+      const float cn = p.cnorm[c];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s = (qn[r] + cn) - 2.f * acc[r];
+        if (!(s > T[r])) {
+          const int row = 4 * (lane >> 4) + r;
+          const int at = atomicAdd(&L.count[row], 1);
+          if (at < cap) L.slot[row * cap + at] = static_cast<uint64_t>(c);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Pass 3: exact keys of the candidates of this wave's rows, then ranks by counting.
+  int cnt[kRowsPerWave], pre[kRowsPerWave + 1];
+  pre[0] = 0;
+#pragma unroll
+  for (int rr = 0; rr < kRowsPerWave; ++rr) {
+    const int row = kRowsPerWave * wave + rr;
+    const int64_t q = q0 + row;
+    const int c = L.count[row];
+    const bool ok = q < p.nq && c >= p.P && c <= cap;
+    cnt[rr] = ok ? c : 0;
+    pre[rr + 1] = pre[rr] + cnt[rr];
+    if (q < p.nq && lane == 0) p.fallback[q] = ok ? 0 : 1;
+  }
+  const int total = pre[kRowsPerWave];
+  for (int f = lane; f < total; f += 64) {
+    int rr = 0;
+#pragma unroll
+    for (int j = 1; j < kRowsPerWave; ++j) rr += f >= pre[j] ? 1 : 0;
+    const int row = kRowsPerWave * wave + rr;
+    uint64_t* s = L.slot + row * cap + (f - pre[rr]);
+    const uint32_t c = static_cast<uint32_t>(*s);
+    const float dot = exact_dot(L.qs + row * dq, p.centroids + static_cast<int64_t>(c) * dim, dim);
+    *s = make_key((p.qnorm[q0 + row] + p.cnorm[c]) - 2.f * dot, c);
+  }
+  wave_sync();
+  for (int f = lane; f < total; f += 64) {
+    int rr = 0;
+#pragma unroll
+    for (int j = 1; j < kRowsPerWave; ++j) rr += f >= pre[j] ? 1 : 0;
+    const int row = kRowsPerWave * wave + rr;
+    const uint64_t* keys = L.slot + row * cap;
+    const uint64_t key = keys[f - pre[rr]];
+    int rank = 0;
+    for (int j = 0; j < cnt[rr]; ++j) rank += keys[j] < key ? 1 : 0;
+    if (rank < p.P) p.probes[(q0 + row) * p.P + rank] = static_cast<int32_t>(key & 0xffffffffu);
+  }
+}
+
+// Exact scores of every centroid for the flagged queries (one workgroup per query;
+// unflagged queries return at once).
+__global__ __launch_bounds__(256) void k_probe_exact_rows(
+    const float* __restrict__ Q, const float* __restrict__ qn, const float* __restrict__ C,
+    const float* __restrict__ cn, int nlist, int dim, const int32_t* __restrict__ flags,
+    float* __restrict__ S) {
+  const int64_t q = blockIdx.x;
+  if (flags[q] == 0) return;
+  const float* qv = Q + q * dim;
+  const float qnq = qn[q];
+  for (int c = static_cast<int>(threadIdx.x); c < nlist; c += 256) {
+    S[q * nlist + c] = (qnq + cn[c]) - 2.f * seq_dot(qv, C + static_cast<int64_t>(c) * dim, dim);
+  }
+}
+
+// Shape of a launch, or false when the fused probe does not serve these sizes.
+bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
+  if (dim <= 0 || dim > 16 * OVVS_PROBE_MAX_DS4 || nlist <= 0 || nlist > (1 << 24) || P <= 0 ||
+      P > OVVS_PROBE_MAX_P)
+    return false;
+  sh->ntile = (nlist + 15) / 16;
+  sh->gt = (sh->ntile + kMaxChunks - 1) / kMaxChunks;
+  sh->nch = (sh->ntile + sh->gt - 1) / sh->gt;
+  int real = 0;
+  for (int ch = 0; ch < sh->nch; ++ch) real += min(16, nlist - 16 * ch * sh->gt);
+  sh->real_groups = real;
+  if (2 * P > real) return false;
+  sh->cap = P <= 64 ? 256 : OVVS_PROBE_CAP;
+  sh->dq = (dim + 3) & ~3;
+  const size_t area = static_cast<size_t>(kRows) *
+                      (static_cast<size_t>(16 * sh->nch) * 4 > static_cast<size_t>(sh->cap) * 8
+                           ? static_cast<size_t>(16 * sh->nch) * 4
+                           : static_cast<size_t>(sh->cap) * 8);
+  sh->lds = align16(static_cast<size_t>(kRows) * sh->dq * 4) + align16(2 * kRows * 4) + area;
+  return sh->lds <= 160 * 1024;
+}
+
+template <int DS4>
+hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
+  if (sh.lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<DS4>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(sh.lds));
+    if (e != hipSuccess) return e;
+  }
+  const int64_t blocks = (p.nq + kRows - 1) / kRows;
+  hipLaunchKernelGGL(k_probe_mfma<DS4>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads),
+                     sh.lds, stream, p, sh);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t P) {
+  ProbeShape sh;
+  return probe_shape(dim, nlist, P, &sh) ? 1 : 0;
+}
+
+extern "C" size_t ovvs_hip_probe_cmfma_floats(int32_t dim, int32_t nlist) {
+  if (dim <= 0 || dim > 16 * OVVS_PROBE_MAX_DS4 || nlist <= 0) return 0;
+  return static_cast<size_t>((nlist + 15) / 16) * 16 * (16 * ((dim + 15) / 16));
+}
+
+extern "C" void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, float* out) {
+  const int ds4 = (dim + 15) / 16, ntile = (nlist + 15) / 16;
+  for (int t = 0; t < ntile; ++t)
+    for (int s4 = 0; s4 < ds4; ++s4)
+      for (int lane = 0; lane < 64; ++lane)
+        for (int e = 0; e < 4; ++e) {
+          const int s = 4 * s4 + e, k = 4 * s + lane / 16, c = 16 * t + lane % 16;
+          out[((static_cast<size_t>(t) * ds4 + s4) * 64 + lane) * 4 + e] =
+              (c < nlist && k < dim) ? C[static_cast<size_t>(c) * dim + k] : 0.f;
+        }
+}
+
+extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream) {
+  if (!args) return hipErrorInvalidValue;
+  const OvvsProbeArgs& p = *args;
+  if (p.nq <= 0) return hipSuccess;
+  ProbeShape sh;
+  if (!p.queries || !p.qnorm || !p.centroids || !p.cmfma || !p.cnorm || !p.probes ||
+      !p.fallback || p.nq > 0x7fffffff || !probe_shape(p.dim, p.nlist, p.P, &sh))
+    return hipErrorInvalidValue;
+  switch ((p.dim + 15) / 16) {
+    case 1: return launch_probe<1>(p, sh, stream);
+    case 2: return launch_probe<2>(p, sh, stream);
+    case 3: return launch_probe<3>(p, sh, stream);
+    case 4: return launch_probe<4>(p, sh, stream);
+    case 5: return launch_probe<5>(p, sh, stream);
+    case 6: return launch_probe<6>(p, sh, stream);
+    case 7: return launch_probe<7>(p, sh, stream);
+    default: return launch_probe<8>(p, sh, stream);
+  }
+}
+
+extern "C" hipError_t ovvs_hip_probe_exact_rows(const float* Q, const float* qn, int64_t nq,
+                                                const float* C, const float* cn, int32_t nlist,
+                                                int32_t dim, const int32_t* flags, float* S,
+                                                hipStream_t stream) {
+  if (nq <= 0) return hipSuccess;
+  if (!Q || !qn || !C || !cn || !flags || !S || nlist <= 0 || dim <= 0 || nq > 0x7fffffff)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_probe_exact_rows, dim3(static_cast<uint32_t>(nq)), dim3(256), 0, stream,
+                     Q, qn, C, cn, nlist, dim, flags, S);
+  return hipGetLastError();
+}

@@ -1,0 +1,114 @@
+"""The matrix-core coarse probe (ovvs_amd/csrc/probe.hip) against the oracle.
+
+Searches with dim <= 128, nprobe <= 256 and at least 2 * nprobe groups of
+centroids take the fused probe: approximate fp32 matrix-core scores, a proven
+candidate bound, exact re-score of the candidates. Everything else takes the
+exact score-matrix route. These cases sit in the fused regime (padded dims,
+nlist not a multiple of 16, the largest nprobe) and require results bit-identical
+to the oracle's, including queries whose candidates exceed the re-score capacity
+(tied centroids) and so go through the exact fallback in the same batch as
+ordinary queries.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import assert_results_match
+from oracle.pyoracle import Oracle, read_ipq1
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+@pytest.fixture(scope="module")
+def res(ovvs):
+    r = ovvs.Resources()
+    if not r.gpu_available():
+        pytest.fail("no GPU visible: gpu tests must run on the MI355X box")
+    return r
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _mixture(rng, n, dim, centers):
+    return (centers[rng.integers(0, len(centers), n)] +
+            0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+
+
+def _check(ix, orc, q, k, nprobe, krefine, label):
+    ids, d = ix.search(q, k, nprobe, krefine)
+    oids, od = orc.search(q, k, nprobe, krefine)
+    assert_results_match(ids, d, oids, od, label=label)
+    assert np.array_equal(_bits(d), _bits(od)), label
+
+
+@pytest.mark.parametrize("dim,pq_m,nlist,nprobes", [
+    (96, 24, 1024, (8, 32, 128)),
+    (40, 10, 1000, (16, 64)),
+    (128, 32, 2048, (64, 256)),
+    (8, 4, 700, (8, 40)),
+])
+def test_matrix_core_probe_matches_oracle(ovvs, res, tmp_path, dim, pq_m, nlist, nprobes):
+    rng = np.random.default_rng(dim * 1000 + nlist)
+    centers = rng.standard_normal((256, dim)).astype(np.float32)
+    data = _mixture(rng, 30000, dim, centers)
+    q = _mixture(rng, 300, dim, centers)
+    say("build", dict(dim=dim, pq_m=pq_m, nlist=nlist))
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=pq_m, pq_nbits=8, resources=res)
+    p = tmp_path / "probe.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for nprobe in nprobes:
+        for k, krefine in [(10, 32), (100, 300)]:
+            say("search", dict(nprobe=nprobe, k=k, krefine=krefine))
+            _check(ix, orc, q, k, nprobe, krefine, f"d{dim} l{nlist} p{nprobe} k{k}")
+    ix.close()
+
+
+def test_probe_fallback_for_tied_centroids(ovvs, res, tmp_path):
+    """700 identical centroids tie every approximate score near them, so queries
+    there have more candidates than the re-score capacity and are ranked by the
+    exact fallback; the other queries of the batch stay on the fused probe.
+    With every centroid identical, all queries fall back and the probes are the
+    first nprobe centroids by ordinal."""
+    rng = np.random.default_rng(5)
+    dim, nlist = 32, 1024
+    centers = rng.standard_normal((128, dim)).astype(np.float32)
+    data = _mixture(rng, 20000, dim, centers)
+    say("build tied-centroid index")
+    built = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=8, pq_nbits=8, resources=res)
+    p = tmp_path / "base.ipq1"
+    built.serialize(p)
+    built.close()
+    base = read_ipq1(p)
+
+    base.centroids[100:800] = base.centroids[100]
+    tied = tmp_path / "tied.ipq1"
+    tied.write_bytes(base.to_bytes())
+    ix = ovvs.neighbors.ivf_pq.load(tied, resources=res)
+    orc = Oracle(read_ipq1(tied))
+    near = (base.centroids[100] + 0.01 * rng.standard_normal((100, dim))).astype(np.float32)
+    q = np.concatenate([near, _mixture(rng, 100, dim, centers)])
+    q = q[rng.permutation(len(q))]
+    for nprobe in (4, 16, 64):
+        say("tied search", nprobe)
+        _check(ix, orc, q, 10, nprobe, 32, f"tied p{nprobe}")
+    ix.close()
+
+    base.centroids[:] = base.centroids[0]
+    same = tmp_path / "same.ipq1"
+    same.write_bytes(base.to_bytes())
+    ix = ovvs.neighbors.ivf_pq.load(same, resources=res)
+    orc = Oracle(read_ipq1(same))
+    say("all-identical search")
+    _check(ix, orc, q, 10, 16, 64, "all identical")
+    ix.close()

@@ -181,3 +181,17 @@ def test_checks_catch_a_contracted_oracle(ref_cases, tmp_path):
             fused = ((r - ix.codebooks.astype(np.float64)) ** 2).sum(-1).astype(np.float32)
             mismatches += int(np.count_nonzero(_bits(fused) != _bits(exact)))
     assert mismatches > 0
+
+
+def test_ipq1_writer_round_trips_reference_files(ref_cases, tmp_path):
+    """Ipq1.to_bytes (used to write indexes with hand-made centroids) reproduces
+    every reference-written file byte for byte."""
+    manifest, arrays = ref_cases
+    for case in manifest:
+        raw = arrays[f"{case['name']}/ipq1"].tobytes()
+        ix = read_ipq1(write_case_ipq1(case, arrays, tmp_path))
+        assert ix.to_bytes() == raw, case["name"]
+    legacy = (GOLDEN / "legacy_ipq1_v1.bin").read_bytes()
+    p = tmp_path / "legacy.ipq1"
+    p.write_bytes(legacy)
+    assert read_ipq1(p).to_bytes() == legacy
