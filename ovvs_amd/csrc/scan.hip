@@ -177,10 +177,78 @@ __device__ __forceinline__ float key_score(uint64_t key) {
 
 // Builds the table slice of subspaces [m0, m0 + mb) into LDS: entry
 // (m - m0) * ks + j = sum_u (r[m*dsub+u] - B[m][j][u])^2, left to right from +0.
+// Codeword u of a DSUB-float codebook entry, loaded in one piece (entries are
+// DSUB * 4-byte aligned).
+template <int DSUB>
+struct Codeword {
+  float v[DSUB];
+  __device__ __forceinline__ void load(const float* __restrict__ p) {
+    if constexpr (DSUB == 1) {
+      v[0] = p[0];
+    } else if constexpr (DSUB == 2) {
+      const float2 x = *reinterpret_cast<const float2*>(p);
+      v[0] = x.x;
+      v[1] = x.y;
+    } else {
+#pragma unroll
+      for (int h = 0; h < DSUB / 4; ++h) {
+        const float4 x = reinterpret_cast<const float4*>(p)[h];
+        v[4 * h + 0] = x.x;
+        v[4 * h + 1] = x.y;
+        v[4 * h + 2] = x.z;
+        v[4 * h + 3] = x.w;
+      }
+    }
+  }
+};
+
+// build_slice for ks == 256: thread j computes entry (i, j) of every subspace i of
+// the slice; codebook loads are issued a group of subspaces (16 floats) at a time
+// ahead of the arithmetic.
+template <int DSUB, bool F16>
+__device__ __forceinline__ void build_slice_256(const float* resid,
+                                                const float* __restrict__ codebooks, int m0,
+                                                int mb, float* lut32, uint16_t* lut16) {
+  constexpr int kGroup = DSUB <= 2 ? kBlock : 16 / DSUB;
+  const int j = static_cast<int>(threadIdx.x);
+  const float* __restrict__ cb = codebooks + (static_cast<int64_t>(m0) * 256 + j) * DSUB;
+#pragma unroll
+  for (int g0 = 0; g0 < kBlock; g0 += kGroup) {
+    Codeword<DSUB> cw[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      if (g0 + i < mb) cw[i].load(cb + (g0 + i) * 256 * DSUB);
+    }
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      if (g0 + i < mb) {
+        const float* r = resid + (m0 + g0 + i) * DSUB;
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < DSUB; ++u) {
+          const float t = r[u] - cw[i].v[u];
+          acc = acc + t * t;
+        }
+        if (F16) {
+          lut16[(g0 + i) * 256 + j] = __half_as_ushort(__float2half_rn(acc));
+        } else {
+          lut32[(g0 + i) * 256 + j] = acc;
+        }
+      }
+    }
+  }
+}
+
 template <int DSUB, bool F16>
 __device__ __forceinline__ void build_slice(const float* resid, const float* __restrict__ codebooks,
                                             int m0, int mb, int ks, int ks_log2, int dsub,
                                             float* lut32, uint16_t* lut16) {
+  if constexpr (DSUB == 1 || DSUB == 2 || DSUB == 4 || DSUB == 8) {
+    if (ks == 256) {
+      build_slice_256<DSUB, F16>(resid, codebooks, m0, mb, lut32, lut16);
+      return;
+    }
+  }
   const int d = DSUB > 0 ? DSUB : dsub;
   const int slice = mb << ks_log2;
   for (int e = threadIdx.x; e < slice; e += 256) {
@@ -356,7 +424,19 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           const uint2 w = *reinterpret_cast<const uint2*>(row0 + i * row_step);
           const uint32_t wv[2] = {w.x, w.y};
           float acc = s[i];
-          if (mb == kBlock) {
+          if (mb == kBlock && ks_log2 == 8) {
+            // All eight table reads are independent: issue them before the
+            // left-to-right additions.
+            float v[kBlock];
+#pragma unroll
+            for (int j = 0; j < kBlock; ++j) {
+              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+              v[j] = F16 ? __half2float(__ushort_as_half(lut16[j * 256 + code]))
+                         : lut32[j * 256 + code];
+            }
+#pragma unroll
+            for (int j = 0; j < kBlock; ++j) acc = acc + v[j];
+          } else if (mb == kBlock) {
 #pragma unroll
             for (int j = 0; j < kBlock; ++j) {
               const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
