@@ -536,10 +536,12 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   }
 }
 
-// Shortlists of up to 128 keys fit 5 waves per SIMD without spilling; longer
-// register lists keep the compiler's own allocation.
+// The scan is latency-bound, so shortlists of up to 128 keys run at 8 waves per
+// SIMD (64 VGPRs): the row loop fits without spilling and only the rarely taken
+// shortlist merge keeps a few values in scratch. Longer register lists keep the
+// compiler's own allocation.
 template <int KPL, bool F16>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void k_scan(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   scan_query<KPL, F16>(a, smem);
