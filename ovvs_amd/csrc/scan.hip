@@ -11,7 +11,7 @@
 // step is src/prim/gpu/backend_gpu.cpp:791-1010).
 //
 // Design (one 256-lane workgroup per query, four wave64s):
-//   * Rows are processed in chunks of up to 4096 (16 per lane, partial sums in
+//   * Rows are processed in chunks of up to 2048 (8 per lane, partial sums in
 //     registers) and subspaces in blocks of 8. For each block the workgroup
 //     builds only that block's 8 x ks table slice into LDS (each entry with the
 //     reference's operation order), then every live row adds its 8 entries in
@@ -175,9 +175,7 @@ __device__ __forceinline__ float key_score(uint64_t key) {
   return __uint_as_float(u);
 }
 
-// Builds the table slice of subspaces [m0, m0 + mb) into LDS: entry
-// (m - m0) * ks + j = sum_u (r[m*dsub+u] - B[m][j][u])^2, left to right from +0.
-// Codeword u of a DSUB-float codebook entry, loaded in one piece (entries are
+// The DSUB floats of one codebook entry, loaded in one piece (entries are
 // DSUB * 4-byte aligned).
 template <int DSUB>
 struct Codeword {
@@ -239,6 +237,8 @@ __device__ __forceinline__ void build_slice_256(const float* resid,
   }
 }
 
+// Builds the table slice of subspaces [m0, m0 + mb) into LDS: entry
+// (m - m0) * ks + j = sum_u (r[m*dsub+u] - B[m][j][u])^2, left to right from +0.
 template <int DSUB, bool F16>
 __device__ __forceinline__ void build_slice(const float* resid, const float* __restrict__ codebooks,
                                             int m0, int mb, int ks, int ks_log2, int dsub,
@@ -282,8 +282,12 @@ __device__ __forceinline__ int64_t code_offset(int64_t pos, int b, int nblocks) 
          static_cast<int64_t>(b) * (kTile * kBlock) + (pos % kTile) * kBlock;
 }
 
+// One block's table slice lives in static LDS (its address is then a link-time
+// constant, folded into the table reads' immediate offsets); the rest is dynamic.
+constexpr size_t kLutBytes = static_cast<size_t>(kBlock) * 256 * 4;
+
 struct ScanLayout {
-  size_t lut_bytes;  // one block's table slice; reused for the final cross-wave merge
+  size_t merge_bytes;  // the final cross-wave merge of the wave lists
   size_t resid_off;
   size_t thr_off;
   size_t bufk_off;
@@ -291,12 +295,10 @@ struct ScanLayout {
   size_t total;
 };
 
-__host__ __device__ inline ScanLayout scan_layout(int ks, int dim, int f16, int kpl) {
+__host__ __device__ inline ScanLayout scan_layout(int dim, int kpl) {
   ScanLayout L;
-  const size_t table = round16(static_cast<size_t>(kBlock) * ks * (f16 ? 2u : 4u));
-  const size_t merge = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
-  L.lut_bytes = table > merge ? table : merge;
-  L.resid_off = L.lut_bytes;
+  L.merge_bytes = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
+  L.resid_off = L.merge_bytes;
   L.thr_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
   L.bufk_off = L.thr_off + kWaves * 8;
   L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
@@ -306,9 +308,10 @@ __host__ __device__ inline ScanLayout scan_layout(int ks, int dim, int f16, int 
 
 template <int KPL, bool F16>
 __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char* smem) {
-  const ScanLayout L = scan_layout(a.ks, a.dim, F16 ? 1 : 0, KPL);
-  float* lut32 = reinterpret_cast<float*>(smem);
-  uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem);
+  const ScanLayout L = scan_layout(a.dim, KPL);
+  __shared__ __attribute__((aligned(16))) float s_lut[kLutBytes / 4];
+  float* lut32 = s_lut;
+  uint16_t* lut16 = reinterpret_cast<uint16_t*>(s_lut);
   float* resid = reinterpret_cast<float*>(smem + L.resid_off);
   uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
   const int wave = threadIdx.x >> 6, lane = lane_id();
@@ -561,7 +564,7 @@ hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   } else {
     fn = k_scan_long<KPL, F16>;
   }
-  if (lds > 65536) {
+  if (lds + kLutBytes > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds));
@@ -578,7 +581,8 @@ int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512
 extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
                                           int32_t lut_f16, int32_t K) {
   if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE) return 0;
-  const size_t b = scan_layout(ks, dim, lut_f16 ? 1 : 0, kpl_for(K)).total;
+  (void)lut_f16;
+  const size_t b = scan_layout(dim, kpl_for(K)).total + kLutBytes;
   return b <= 160u * 1024u ? b : 0;
 }
 
@@ -593,8 +597,8 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
       static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
     return hipErrorInvalidValue;
   const int kpl = kpl_for(a.K);
-  const size_t lds = scan_layout(a.ks, a.dim, a.lut_f16 ? 1 : 0, kpl).total;
-  if (lds > 160u * 1024u) return hipErrorInvalidValue;
+  const size_t lds = scan_layout(a.dim, kpl).total;
+  if (lds + kLutBytes > 160u * 1024u) return hipErrorInvalidValue;
   if (a.lut_f16) {
     switch (kpl) {
       case 1: return launch_scan<1, true>(a, lds, stream);
