@@ -421,10 +421,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         const uint8_t* __restrict__ row0 =
             a.codes + code_offset(begin + c0 + threadIdx.x, b, nblocks);
         const int64_t row_step = static_cast<int64_t>(kThreads / kTile) * nblocks * kTile * kBlock;
+        uint2 w_next = make_uint2(0u, 0u);
+        if (alive & 1u) w_next = *reinterpret_cast<const uint2*>(row0);
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) {
+          const uint2 w = w_next;
+          if (i + 1 < kRowsPerLane && ((alive >> (i + 1)) & 1u))
+            w_next = *reinterpret_cast<const uint2*>(row0 + (i + 1) * row_step);
           if (!((alive >> i) & 1u)) continue;
-          const uint2 w = *reinterpret_cast<const uint2*>(row0 + i * row_step);
           const uint32_t wv[2] = {w.x, w.y};
           float acc = s[i];
           if (mb == kBlock && ks_log2 == 8) {
