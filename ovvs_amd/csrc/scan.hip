@@ -306,7 +306,9 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl) {
   return L;
 }
 
-template <int KPL, bool F16>
+// FD > 0: the shape-specialised body for ks = 256, pq_m % 8 == 0 and dsub = FD
+// (every block full, table rows 1 KiB apart); FD = 0: any shape.
+template <int KPL, bool F16, int FD>
 __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char* smem) {
   const ScanLayout L = scan_layout(a.dim, KPL);
   __shared__ __attribute__((aligned(16))) float s_lut[kLutBytes / 4];
@@ -314,7 +316,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(s_lut);
   float* resid = reinterpret_cast<float*>(smem + L.resid_off);
   uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
-  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = lane_id(), tid = static_cast<int>(threadIdx.x);
   uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
   int32_t* bufp = reinterpret_cast<int32_t*>(smem + L.bufp_off) + wave * kBufCap;
 
@@ -324,6 +327,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   const int ks_log2 = __ffs(ks) - 1;
   const int K = a.K;
   const int nblocks = (a.pq_m + kBlock - 1) / kBlock;
+  // Bytes of one 64-row code tile, and the distance between a lane's rows i, i+1.
+  const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
+  const uint32_t row_step = (kThreads / kTile) * tile_bytes;
 
   uint64_t lk[KPL];
   int32_t lp[KPL];
@@ -372,15 +378,22 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 
     for (int64_t c0 = 0; c0 < rows; c0 += kChunkRows) {
       const int chunk = static_cast<int>(rows - c0 < kChunkRows ? rows - c0 : kChunkRows);
+      // Chunk rows are packed positions cpos + r, r = tid + i * kThreads. Their
+      // codes are addressed from a uniform base (the chunk's first tile) plus a
+      // 32-bit per-lane offset; rows i and i+1 of a lane are 4 tiles apart.
+      const int64_t cpos = begin + c0;
+      const uint8_t* __restrict__ cbase = a.codes + (cpos >> 6) * tile_bytes;
+      const uint32_t lrow = static_cast<uint32_t>(cpos & (kTile - 1)) + static_cast<uint32_t>(tid);
+      const uint32_t loff = (lrow >> 6) * tile_bytes + (lrow & (kTile - 1)) * kBlock;
       float s[kRowsPerLane];
       uint32_t alive = 0;
 #pragma unroll
       for (int i = 0; i < kRowsPerLane; ++i) {
         s[i] = 0.f;
-        const int r = static_cast<int>(threadIdx.x) + i * kThreads;
+        const int r = tid + i * kThreads;
         bool ok = r < chunk;
         if (ok && a.bitset) {
-          const int64_t id = a.ids[begin + c0 + r];
+          const int64_t id = a.ids[cpos + r];
           ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
         }
         alive |= static_cast<uint32_t>(ok) << i;
@@ -390,7 +403,10 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         // Also the barrier that retires the previous block's table slice (and
         // publishes resid for the first block).
         if (!__syncthreads_or(alive != 0)) break;
-        const int mb = a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock;
+        const int mb = FD > 0 ? kBlock : (a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock);
+        if constexpr (FD > 0) {
+          build_slice_256<FD, F16>(resid, a.codebooks, b * kBlock, kBlock, lut32, lut16);
+        } else {
         switch (a.dsub) {
           case 1:
             build_slice<1, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 1, lut32, lut16);
@@ -408,6 +424,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
             build_slice<0, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, a.dsub, lut32,
                                 lut16);
         }
+        }
         __syncthreads();
         // Prune bound: the smallest K-th key any wave has published. Partial
         // sums are >= +0 (or NaN, never pruned), so comparing floats against the
@@ -416,22 +433,23 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) tmin = wave_thr[w] < tmin ? wave_thr[w] : tmin;
         const float thr_f = key_score(tmin);
-        // Rows i and i+1 of a lane are kThreads = 4 tiles apart: one base
-        // address plus a uniform stride reaches all of them.
-        const uint8_t* __restrict__ row0 =
-            a.codes + code_offset(begin + c0 + threadIdx.x, b, nblocks);
-        const int64_t row_step = static_cast<int64_t>(kThreads / kTile) * nblocks * kTile * kBlock;
+        const uint8_t* __restrict__ bbase = cbase + b * (kTile * kBlock);
+        // Recompute the per-row offsets in every block (one 32-bit add each)
+        // rather than let them be hoisted out of the block loop as 64-bit
+        // addresses held in registers across it.
+        uint32_t loff_b = loff;
+        asm volatile("" : "+v"(loff_b));
         uint2 w_next = make_uint2(0u, 0u);
-        if (alive & 1u) w_next = *reinterpret_cast<const uint2*>(row0);
+        if (alive & 1u) w_next = *reinterpret_cast<const uint2*>(bbase + loff_b);
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) {
           const uint2 w = w_next;
           if (i + 1 < kRowsPerLane && ((alive >> (i + 1)) & 1u))
-            w_next = *reinterpret_cast<const uint2*>(row0 + (i + 1) * row_step);
+            w_next = *reinterpret_cast<const uint2*>(bbase + (loff_b + (i + 1) * row_step));
           if (!((alive >> i) & 1u)) continue;
           const uint32_t wv[2] = {w.x, w.y};
           float acc = s[i];
-          if (mb == kBlock && ks_log2 == 8) {
+          if (FD > 0 || (mb == kBlock && ks_log2 == 8)) {
             // All eight table reads are independent: issue them before the
             // left-to-right additions.
             float v[kBlock];
@@ -443,6 +461,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
             }
 #pragma unroll
             for (int j = 0; j < kBlock; ++j) acc = acc + v[j];
+          } else if constexpr (FD > 0) {
           } else if (mb == kBlock) {
 #pragma unroll
             for (int j = 0; j < kBlock; ++j) {
@@ -467,7 +486,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       for (int i = 0; i < kRowsPerLane; ++i) {
         if (i * kThreads >= chunk) break;
         if (__ballot((alive >> i) & 1u) == 0) continue;
-        const int r = static_cast<int>(threadIdx.x) + i * kThreads;
+        const int r = tid + i * kThreads;
         const bool ok = ((alive >> i) & 1u) != 0;
         const uint64_t key =
             ok ? make_key(s[i], ord_base + static_cast<uint32_t>(c0) + static_cast<uint32_t>(r))
@@ -478,7 +497,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           const int before = __popcll(bal & ((1ull << lane) - 1ull));
           if (pass) {
             bufk[cnt + before] = key;
-            bufp[cnt + before] = static_cast<int32_t>(begin + c0 + r);
+            bufp[cnt + before] = static_cast<int32_t>(cpos) + r;
           }
           cnt += __popcll(bal);
           if (cnt >= 64) flush();
@@ -547,24 +566,31 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 // SIMD (64 VGPRs): the row loop fits without spilling and only the rarely taken
 // shortlist merge keeps a few values in scratch. Longer register lists keep the
 // compiler's own allocation.
-template <int KPL, bool F16>
+template <int KPL, bool F16, int FD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  scan_query<KPL, F16>(a, smem);
+  scan_query<KPL, F16, FD>(a, smem);
 }
 
 template <int KPL, bool F16>
 __global__ __launch_bounds__(kThreads) void k_scan_long(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  scan_query<KPL, F16>(a, smem);
+  scan_query<KPL, F16, 0>(a, smem);
 }
 
 template <int KPL, bool F16>
 hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   void (*fn)(OvvsScanArgs);
   if constexpr (KPL <= 2) {
-    fn = k_scan<KPL, F16>;
+    const bool shaped = a.ks == 256 && a.pq_m % kBlock == 0;
+    switch (shaped ? a.dsub : 0) {
+      case 1: fn = k_scan<KPL, F16, 1>; break;
+      case 2: fn = k_scan<KPL, F16, 2>; break;
+      case 4: fn = k_scan<KPL, F16, 4>; break;
+      case 8: fn = k_scan<KPL, F16, 8>; break;
+      default: fn = k_scan<KPL, F16, 0>;
+    }
   } else {
     fn = k_scan_long<KPL, F16>;
   }
