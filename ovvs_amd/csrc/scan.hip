@@ -290,6 +290,7 @@ struct ScanLayout {
   size_t merge_bytes;  // the final cross-wave merge of the wave lists
   size_t resid_off;
   size_t thr_off;
+  size_t any_off;
   size_t bufk_off;
   size_t bufp_off;
   size_t total;
@@ -300,7 +301,8 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl) {
   L.merge_bytes = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
   L.resid_off = L.merge_bytes;
   L.thr_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
-  L.bufk_off = L.thr_off + kWaves * 8;
+  L.any_off = L.thr_off + kWaves * 8;
+  L.bufk_off = L.any_off + round16(kWaves * 4);
   L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
   L.total = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
   return L;
@@ -316,6 +318,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(s_lut);
   float* resid = reinterpret_cast<float*>(smem + L.resid_off);
   uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
+  // Per wave: 1 while any of its rows of the current chunk is alive.
+  int32_t* wave_any = reinterpret_cast<int32_t*>(smem + L.any_off);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = lane_id(), tid = static_cast<int>(threadIdx.x);
   uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
@@ -386,7 +390,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const uint32_t lrow = static_cast<uint32_t>(cpos & (kTile - 1)) + static_cast<uint32_t>(tid);
       const uint32_t loff = (lrow >> 6) * tile_bytes + (lrow & (kTile - 1)) * kBlock;
       float s[kRowsPerLane];
-      uint32_t alive = 0;
+      // live[i]: the wave's lanes whose row i is still a shortlist candidate
+      // (a wave-uniform lane mask, used directly as the execution mask).
+      uint64_t live[kRowsPerLane];
 #pragma unroll
       for (int i = 0; i < kRowsPerLane; ++i) {
         s[i] = 0.f;
@@ -396,13 +402,23 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           const int64_t id = a.ids[cpos + r];
           ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
         }
-        alive |= static_cast<uint32_t>(ok) << i;
+        live[i] = __builtin_amdgcn_ballot_w64(ok);
+      }
+      {
+        uint64_t any = 0;
+#pragma unroll
+        for (int i = 0; i < kRowsPerLane; ++i) any |= live[i];
+        if (lane == 0) wave_any[wave] = any != 0 ? 1 : 0;
       }
 
       for (int b = 0; b < nblocks; ++b) {
-        // Also the barrier that retires the previous block's table slice (and
-        // publishes resid for the first block).
-        if (!__syncthreads_or(alive != 0)) break;
+        // Retires the previous block's table slice, publishes the waves' live
+        // flags (and resid, for the first block).
+        __syncthreads();
+        int any = wave_any[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) any |= wave_any[w];
+        if (!any) break;
         const int mb = FD > 0 ? kBlock : (a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock);
         if constexpr (FD > 0) {
           build_slice_256<FD, F16>(resid, a.codebooks, b * kBlock, kBlock, lut32, lut16);
@@ -440,13 +456,17 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         uint32_t loff_b = loff;
         asm volatile("" : "+v"(loff_b));
         uint2 w_next = make_uint2(0u, 0u);
-        if (alive & 1u) w_next = *reinterpret_cast<const uint2*>(bbase + loff_b);
+        if (__builtin_amdgcn_inverse_ballot_w64(live[0]))
+          w_next = *reinterpret_cast<const uint2*>(bbase + loff_b);
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) {
           const uint2 w = w_next;
-          if (i + 1 < kRowsPerLane && ((alive >> (i + 1)) & 1u))
+          if (i + 1 < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[i + 1]))
             w_next = *reinterpret_cast<const uint2*>(bbase + (loff_b + (i + 1) * row_step));
-          if (!((alive >> i) & 1u)) continue;
+          // Uniform skip; within a live row every lane scores its code word (a
+          // dead lane's word is an earlier row's or zero, so its table reads stay
+          // in the slice) and only live lanes keep the result.
+          if (live[i] == 0) continue;
           const uint32_t wv[2] = {w.x, w.y};
           float acc = s[i];
           if (FD > 0 || (mb == kBlock && ks_log2 == 8)) {
@@ -477,17 +497,23 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
             }
           }
           s[i] = acc;
-          if (acc > thr_f) alive &= ~(1u << i);
+          live[i] &= __builtin_amdgcn_ballot_w64(!(acc > thr_f));
         }
+        // Read by every wave after the next block's first barrier; this wave
+        // writes it again only after that block's second barrier.
+        uint64_t any_left = 0;
+#pragma unroll
+        for (int i = 0; i < kRowsPerLane; ++i) any_left |= live[i];
+        if (lane == 0) wave_any[wave] = any_left != 0 ? 1 : 0;
       }
 
       // Rows still alive carry their complete score: offer them to the wave's list.
 #pragma unroll
       for (int i = 0; i < kRowsPerLane; ++i) {
         if (i * kThreads >= chunk) break;
-        if (__ballot((alive >> i) & 1u) == 0) continue;
+        if (live[i] == 0) continue;
         const int r = tid + i * kThreads;
-        const bool ok = ((alive >> i) & 1u) != 0;
+        const bool ok = __builtin_amdgcn_inverse_ballot_w64(live[i]);
         const uint64_t key =
             ok ? make_key(s[i], ord_base + static_cast<uint32_t>(c0) + static_cast<uint32_t>(r))
                : kNoKey;
