@@ -15,9 +15,13 @@ The JSON line also carries:
                 divided by its average duration (HIP events on the library's
                 stream), against the 8 TB/s HBM peak;
   cpu_baseline  the reference library's own CPU search (oracle/_ref, built
-                from /root/reference) on the same index, single thread, on a
-                bounded query sample, with id parity against the GPU answers;
-  recall_at_10  against exact brute force (fp32 on the GPU, torch matmul).
+                from /root/reference) on the same index: the whole batch over
+                --cpu-threads threads (one Resources each, the reference's
+                concurrency model; `value`, `cores`) and one thread on a
+                --cpu-sample prefix (`value_1_thread`);
+  parity_vs_reference  the whole batch, GPU fp32-table answers against the
+                reference's: identical rows, bit-identical distances;
+  recall_at_k   against exact brute force (fp32 on the GPU, torch matmul).
 Progress lines go to stderr; stdout carries exactly one JSON line.
 """
 
@@ -102,7 +106,13 @@ def same_up_to_ties(ids_a, d_a, ids_b, d_b, rel=1e-5):
     return bad
 
 
-def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample):
+def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample, threads,
+                 lut_f16, ovvs_amd):
+    """The reference library (oracle/_ref, FORCE_CPU) on this host: one thread on a
+    `sample`-query prefix, then `threads` threads (one Resources each over query
+    shards, the reference's concurrency model) on the whole batch. Parity compares
+    the whole batch with the GPU's fp32-table results (for binary16-table configs
+    the GPU search is repeated with fp32 tables, the reference's only precision)."""
     from oracle.pyoracle import REF_SO, Reference
 
     if not REF_SO.exists():
@@ -115,25 +125,40 @@ def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample):
         rc, h = ref.load(path)
         if rc != 0:
             raise RuntimeError(f"reference deserialize failed: {rc}")
-    q = np.ascontiguousarray(queries[:sample])
-    log(f"cpu baseline: reference CPU search of {len(q)} queries, 1 thread")
-    ref.search(h, q[:8], k, nprobe, krefine)  # warm-up
+    q1 = np.ascontiguousarray(queries[:sample])
+    log(f"cpu baseline: reference CPU search of {len(q1)} queries, 1 thread")
+    ref.search(h, q1[:8], k, nprobe, krefine)  # warm-up
     t = time.perf_counter()
-    rc, rids, rd = ref.search(h, q, k, nprobe, krefine)
-    dt = time.perf_counter() - t
+    rc, _, _ = ref.search(h, q1, k, nprobe, krefine)
+    dt1 = time.perf_counter() - t
     if rc != 0:
         raise RuntimeError(f"reference search failed: {rc}")
+    log(f"cpu baseline: reference CPU search of {len(queries)} queries, {threads} threads")
+    t = time.perf_counter()
+    rc, rids, rd = ref.search_threads(h, queries, k, nprobe, krefine, threads)
+    dtn = time.perf_counter() - t
+    if rc != 0:
+        raise RuntimeError(f"reference threaded search failed: {rc}")
     ref.destroy(h)
     ref.close()
-    exact_rows = int(np.sum(np.all(rids == gpu_ids[:sample], axis=1)))
-    mism = same_up_to_ties(gpu_ids[:sample], gpu_d[:sample], rids, rd)
-    dist_err = float(np.max(np.abs(gpu_d[:sample].astype(np.float64) - rd) /
-                            np.maximum(1.0, np.abs(rd)))) if np.all(np.isfinite(rd)) else None
-    base = {"value": len(q) / dt, "unit": "queries/s", "cores": 1, "kind": "reference",
-            "sample": f"first {len(q)} of the {len(queries)}-query batch, same index, "
-                      f"reference ovvsIvfPqSearch FORCE_CPU, median of 1 timed call "
-                      f"({dt:.1f} s)"}
-    parity = {"sample_queries": len(q), "rows_identical": exact_rows,
+    if lut_f16:
+        gpu_ids, gpu_d = index.search_ex(queries, k, nprobe, krefine,
+                                         lut_dtype=ovvs_amd.DTYPE_F32)
+    exact_rows = int(np.sum(np.all(rids == gpu_ids, axis=1)))
+    bits_equal = bool(np.array_equal(np.ascontiguousarray(gpu_d).view(np.uint32),
+                                     np.ascontiguousarray(rd).view(np.uint32)))
+    mism = same_up_to_ties(gpu_ids, gpu_d, rids, rd)
+    fin = np.isfinite(rd)
+    dist_err = float(np.max(np.abs(gpu_d[fin].astype(np.float64) - rd[fin]) /
+                            np.maximum(1.0, np.abs(rd[fin])))) if fin.any() else 0.0
+    base = {"value": len(queries) / dtn, "unit": "queries/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"the whole {len(queries)}-query batch over {threads} threads "
+                      f"({dtn:.1f} s wall), same index, reference ovvsIvfPqSearch FORCE_CPU",
+            "value_1_thread": len(q1) / dt1,
+            "sample_1_thread": f"first {len(q1)} queries, 1 thread ({dt1:.1f} s)"}
+    parity = {"queries": len(queries), "tables": "f32",
+              "rows_identical": exact_rows, "distances_bit_identical": bits_equal,
               "rows_differing_beyond_ties": mism, "max_rel_distance_error": dist_err}
     return base, parity
 
@@ -146,7 +171,10 @@ def main() -> int:
     ap.add_argument("--config", default="c2")
     ap.add_argument("--nq", type=int, default=None, help="query batch (default: config's)")
     ap.add_argument("--krefine", type=int, default=None, help="default: k")
-    ap.add_argument("--cpu-sample", type=int, default=1000)
+    ap.add_argument("--cpu-sample", type=int, default=1000,
+                    help="queries of the single-thread reference timing")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
+                    help="threads of the whole-batch reference timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -252,7 +280,8 @@ def main() -> int:
     cpu, parity = (None, None)
     if not args.no_cpu_baseline:
         cpu, parity = cpu_baseline(index, queries, gpu_ids, gpu_d, k, cfg.nprobe, krefine,
-                                   min(args.cpu_sample, nq))
+                                   min(args.cpu_sample, nq), args.cpu_threads, cfg.lut_f16,
+                                   ovvs_amd)
         if cpu:
             log(f"cpu baseline {cpu['value']:,.1f} QPS; parity {parity}")
 
@@ -291,7 +320,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "stage_ms": stage_ms,
         "qps_host_io": qps_host,
-        "recall_at_10": rec,
+        "recall_at_k": rec,
+        "recall_k": k,
         "parity_vs_reference": parity,
     }
     print(json.dumps(line), flush=True)

@@ -289,6 +289,41 @@ class Reference:
                                       _i64p(ids), _f32p(d))
         return rc, ids, d
 
+    def search_threads(self, h, queries, k, nprobe, krefine, threads):
+        """The reference's documented concurrency model (include/ovvs/ovvs.h:165-166):
+        `threads` threads, each with its own Resources (FORCE_CPU), search contiguous
+        query shards of one shared index. ctypes releases the GIL during each call."""
+        import threading
+
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        nq = q.shape[0]
+        ids = np.full((nq, k), -9, dtype=np.int64)
+        d = np.full((nq, k), -9.0, dtype=np.float32)
+        bounds = np.linspace(0, nq, threads + 1).astype(np.int64)
+        rcs = [0] * threads
+        handles = []
+        for _ in range(threads):
+            r = c_void_p()
+            assert self.lib.ovvsResourcesCreate(ctypes.byref(r)) == 0
+            assert self.lib.ovvsResourcesSetPolicy(r, FORCE_CPU) == 0
+            handles.append(r)
+
+        def work(t):
+            a, b = int(bounds[t]), int(bounds[t + 1])
+            if b > a:
+                rcs[t] = self.lib.ovvsIvfPqSearch(handles[t], h, _f32p(q[a:b]), b - a, k, nprobe,
+                                                  krefine, None, _i64p(ids[a:b]), _f32p(d[a:b]))
+
+        pool = [threading.Thread(target=work, args=(t,)) for t in range(threads)]
+        for t in pool:
+            t.start()
+        for t in pool:
+            t.join()
+        for r in handles:
+            self.lib.ovvsResourcesDestroy(r)
+        rc = next((x for x in rcs if x != 0), 0)
+        return rc, ids, d
+
     def destroy(self, h):
         if h:
             self.lib.ovvsIvfPqDestroy(h)

@@ -8,10 +8,14 @@
 //
 // Device pipeline per call, all on the Resources stream:
 //   1. query norms                          ovvs_hip_row_norms
-//   2. coarse scores, chunked over queries  ovvs_hip_coarse_scores
-//   3. probe selection                      ovvs_hip_select_topk
-//   4. fused LUT + code scan + shortlist    ovvs_hip_scan
-//   5. exact re-rank + final select         ovvs_hip_refine
+//   2. probe selection, either
+//      a. matrix-core probe with exact       ovvs_hip_probe_mfma, then for the queries
+//         re-score (dim <= 128, enough        it flags ovvs_hip_probe_exact_rows +
+//         centroid groups)                    ovvs_hip_select_topk_flagged
+//      b. exact coarse scores, chunked over  ovvs_hip_coarse_scores +
+//         queries, and row selection         ovvs_hip_select_topk
+//   3. fused LUT + code scan + shortlist    ovvs_hip_scan
+//   4. exact re-rank + final select         ovvs_hip_refine
 // There is no host compute path: without a usable GPU the call fails with
 // OVVS_STATUS_DEVICE_UNAVAILABLE.
 #include <hip/hip_runtime_api.h>
@@ -111,7 +115,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
   // OVVS_HIP_MAX_REFINE bounds krefine and k.
   if (R > OVVS_HIP_MAX_REFINE || P > OVVS_HIP_MAX_PROBES ||
       ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16, R) == 0 ||
-      nq > 0x7fffffff) {
+      nq > 0x7fffffff || ix.n > 0x7fffffff) {
     return OVVS_STATUS_DEVICE_UNAVAILABLE;
   }
 
@@ -234,6 +238,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.ks = ix.pq_ks;
     sa.dsub = ix.dsub;
     sa.code_blocks = dv.code_blocks;
+    sa.nlist = ix.nlist;
     sa.list_offsets = dv.offsets.as<int64_t>();
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();
@@ -255,6 +260,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.metric = static_cast<int32_t>(ix.metric);
     ra.dataset = dv.dataset.as<float>();
     ra.xnorm = dv.xnorm.as<float>();
+    ra.n = ix.n;
     ra.ids = dv.ids.as<int64_t>();
     ra.K = R;
     ra.short_pos = d_spos;
@@ -262,6 +268,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.k = k;
     ra.out_ids = d_oid;
     ra.out_dist = d_odist;
+    ra.invalid = d_counters + 3;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
     work.kernel_launches += 3 + 2 * chunks;
@@ -278,6 +285,11 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     }
     ovvs::saturating_add(work.wait_calls, 1);
     SEARCH_HIP(hipStreamSynchronize(s));
+    unsigned long long counters[4];
+    std::memcpy(counters, pin, sizeof(counters));
+    // A probe id or shortlist position out of range is an internal error: the
+    // kernels count it instead of dereferencing it, and nothing is published.
+    if (counters[3] != 0) return OVVS_STATUS_ERROR;
 
     // Success: publish the outputs.
     if (device_io) {
@@ -290,8 +302,6 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       std::memcpy(distances, pin + 32 + nqk * 8, nqk * 4);
     }
 
-    unsigned long long counters[4];
-    std::memcpy(counters, pin, sizeof(counters));
     ovvsIvfPqSearchStatsV1 d{};
     d.successful_calls = 1;
     d.blocks = chunks;

@@ -108,6 +108,7 @@ struct OvvsScanArgs {
   int32_t ks;                  // power of two, 16..256
   int32_t dsub;
   int32_t code_blocks;         // ceil(pq_m / OVVS_CODE_BLOCK)
+  int32_t nlist;
   const int64_t* list_offsets; // [nlist + 1]
   const uint8_t* codes;        // tiled list-major codes, see OVVS_CODE_TILE_ROWS
   const int64_t* ids;          // [n], list-major
@@ -117,8 +118,8 @@ struct OvvsScanArgs {
   uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
   int32_t* out_pos;            // [nq * K] packed positions
   int32_t* out_count;          // [nq]
-  unsigned long long* counters; // [3]: += scanned rows, += non-empty (query, list) tasks,
-                                //      += shortlist entries
+  unsigned long long* counters; // [4]: += scanned rows, += non-empty (query, list) tasks,
+                                //      += shortlist entries, += probe ids out of range
 };
 
 // Fused residual-LUT build (in LDS) + ADC code scan + per-query shortlist of
@@ -136,6 +137,7 @@ struct OvvsRefineArgs {
   int32_t metric;         // ovvsMetric
   const float* dataset;   // [n * dim], row = id
   const float* xnorm;     // [n]
+  int64_t n;
   const int64_t* ids;     // [n] list-major (packed position -> id)
   int32_t K;              // shortlist stride
   const int32_t* short_pos;    // [nq * K]
@@ -143,6 +145,7 @@ struct OvvsRefineArgs {
   int64_t k;              // outputs per query
   int64_t* out_ids;       // [nq * k]
   float* out_dist;        // [nq * k]
+  unsigned long long* invalid;  // += shortlist entries whose position or id is out of range
 };
 
 // Exact re-rank of each query's shortlist by the index metric and final select

@@ -73,15 +73,22 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a) {
   int M = 1;
   while (M < cnt) M <<= 1;
   for (int i = lane; i < M; i += 64) {
+    uint64_t key = kNoKey;
     if (i < cnt) {
-      const int64_t id = a.ids[a.short_pos[q * a.K + i]];
-      const float v = metric_value(a.metric, qv, a.dataset + id * a.dim, a.dim, a.qnorm[q],
-                                   a.xnorm[id]);
-      keys[i] = make_key(v, static_cast<uint32_t>(i));
-      vals[i] = v;
-    } else {
-      keys[i] = kNoKey;
+      // Positions come from the scan; one out of range is reported (the search
+      // then fails) instead of being dereferenced.
+      const int32_t pos = a.short_pos[q * a.K + i];
+      const int64_t id = (pos >= 0 && pos < a.n) ? a.ids[pos] : -1;
+      if (id >= 0 && id < a.n) {
+        const float v = metric_value(a.metric, qv, a.dataset + id * a.dim, a.dim, a.qnorm[q],
+                                     a.xnorm[id]);
+        key = make_key(v, static_cast<uint32_t>(i));
+        vals[i] = v;
+      } else {
+        atomicAdd(a.invalid, 1ull);
+      }
     }
+    keys[i] = key;
   }
   __syncthreads();
   for (int k = 2; k <= M; k <<= 1) {
@@ -103,7 +110,7 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a) {
   for (int64_t t = lane; t < a.k; t += 64) {
     int64_t id = -1;
     float d = __builtin_inff();
-    if (t < kk) {
+    if (t < kk && keys[t] != kNoKey) {
       const int i = static_cast<int>(keys[t] & 0xffffffffu);
       id = a.ids[a.short_pos[q * a.K + i]];
       d = a.metric == kIP ? -vals[i] : vals[i];
@@ -120,7 +127,8 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
   const OvvsRefineArgs& a = *args;
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.qnorm || !a.dataset || !a.xnorm || !a.ids || !a.short_pos ||
-      !a.short_count || !a.out_ids || !a.out_dist || a.dim <= 0 || a.K <= 0 ||
+      !a.short_count || !a.out_ids || !a.out_dist || !a.invalid || a.n <= 0 || a.dim <= 0 ||
+      a.K <= 0 ||
       a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq)), dim3(64), 0, stream, a);

@@ -302,7 +302,7 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl) {
   L.resid_off = L.merge_bytes;
   L.thr_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
   L.any_off = L.thr_off + kWaves * 8;
-  L.bufk_off = L.any_off + round16(kWaves * 4);
+  L.bufk_off = L.any_off + round16(2 * kWaves * 4);
   L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
   L.total = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
   return L;
@@ -318,8 +318,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(s_lut);
   float* resid = reinterpret_cast<float*>(smem + L.resid_off);
   uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
-  // Per wave: 1 while any of its rows of the current chunk is alive.
+  // Per wave: 1 while any of its rows of the current chunk is alive, in two
+  // slots used by alternate reads (any_rd is the slot the next read uses; every
+  // wave performs the same sequence of reads). A wave that leaves the block loop
+  // can start the next chunk and write its flag before a slower wave has read
+  // the flags that ended the loop: the write goes to the other slot, and it can
+  // be two reads ahead only after a barrier that the slower wave must reach.
   int32_t* wave_any = reinterpret_cast<int32_t*>(smem + L.any_off);
+  int any_rd = 0;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = lane_id(), tid = static_cast<int>(threadIdx.x);
   uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
@@ -346,6 +352,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int cnt = 0;
   uint32_t ord_base = 0;
   unsigned long long rows_total = 0, tasks = 0;
+  int bad_probe = 0;
   if (lane == 0) wave_thr[wave] = kNoKey;
 
   // Merges the first min(cnt, 64) buffered candidates into the wave's list and
@@ -369,7 +376,11 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   };
 
   for (int p = 0; p < a.P; ++p) {
-    const int l = a.probes[q * a.P + p];
+    int l = a.probes[q * a.P + p];
+    if (static_cast<uint32_t>(l) >= static_cast<uint32_t>(a.nlist)) {
+      bad_probe = 1;  // reported at the end (the search then fails), never dereferenced
+      l = 0;
+    }
     const int64_t begin = a.list_offsets[l];
     const int64_t rows = a.list_offsets[l + 1] - begin;
     if (rows <= 0) continue;
@@ -408,16 +419,17 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         uint64_t any = 0;
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) any |= live[i];
-        if (lane == 0) wave_any[wave] = any != 0 ? 1 : 0;
+        if (lane == 0) wave_any[any_rd * kWaves + wave] = any != 0 ? 1 : 0;
       }
 
       for (int b = 0; b < nblocks; ++b) {
         // Retires the previous block's table slice, publishes the waves' live
         // flags (and resid, for the first block).
         __syncthreads();
-        int any = wave_any[0];
+        int any = wave_any[any_rd * kWaves];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) any |= wave_any[w];
+        for (int w = 1; w < kWaves; ++w) any |= wave_any[any_rd * kWaves + w];
+        any_rd ^= 1;
         if (!any) break;
         const int mb = FD > 0 ? kBlock : (a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock);
         if constexpr (FD > 0) {
@@ -499,12 +511,11 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           s[i] = acc;
           live[i] &= __builtin_amdgcn_ballot_w64(!(acc > thr_f));
         }
-        // Read by every wave after the next block's first barrier; this wave
-        // writes it again only after that block's second barrier.
+        // For the next block's read.
         uint64_t any_left = 0;
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) any_left |= live[i];
-        if (lane == 0) wave_any[wave] = any_left != 0 ? 1 : 0;
+        if (lane == 0) wave_any[any_rd * kWaves + wave] = any_left != 0 ? 1 : 0;
       }
 
       // Rows still alive carry their complete score: offer them to the wave's list.
@@ -584,6 +595,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       atomicAdd(&a.counters[0], rows_total);
       atomicAdd(&a.counters[1], tasks);
       atomicAdd(&a.counters[2], static_cast<unsigned long long>(valid));
+      if (bad_probe) atomicAdd(&a.counters[3], 1ull);
     }
   }
 }
@@ -648,6 +660,7 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
       !a.ids || !a.out_keys || !a.out_pos || !a.out_count || !a.counters || a.nq > 0x7fffffff ||
+      a.nlist <= 0 ||
       a.dim <= 0 || a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 ||
       (a.ks & (a.ks - 1)) != 0 || a.code_blocks != (a.pq_m + kBlock - 1) / kBlock ||
       static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
