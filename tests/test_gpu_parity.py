@@ -148,6 +148,32 @@ def test_random_indexes_against_oracle(ovvs, res, tmp_path):
         ix.close()
 
 
+def test_multi_chunk_lists_against_oracle(ovvs, res, tmp_path):
+    """Lists of several thousand rows span several of the scan's 2048-row chunks,
+    and a tight shortlist (k = krefine = 10) prunes whole chunks after their first
+    block, so waves leave the block loop and start the next chunk at different
+    times. Results must match the oracle on every one of several repeats."""
+    rng = np.random.default_rng(23)
+    dim, n, nlist = 32, 60000, 8
+    centers = rng.standard_normal((16, dim)).astype(np.float32)
+    data = (centers[rng.integers(0, 16, n)] + 0.3 * rng.standard_normal((n, dim))).astype(
+        np.float32)
+    q = (centers[rng.integers(0, 16, 2000)] + 0.3 * rng.standard_normal((2000, dim))).astype(
+        np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=16, pq_nbits=8, resources=res)
+    p = tmp_path / "chunks.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    assert max(len(l) for l in orc.ix.lists) > 3 * 2048
+    oids, od = orc.search(q, 10, 4, 10)
+    for rep in range(3):
+        say("multi-chunk repeat", rep)
+        ids, d = ix.search(q, 10, 4, 10)
+        assert_results_match(ids, d, oids, od, label=f"repeat {rep}")
+        assert np.array_equal(_bits(d), _bits(od)), f"repeat {rep}"
+    ix.close()
+
+
 def test_device_pointer_entry_matches_host_entry(ovvs, res, ref_cases, tmp_path):
     import torch
 
