@@ -107,40 +107,6 @@ __device__ __forceinline__ f32x4 tile_dot(const float (&a)[4 * DS4],
   return acc;
 }
 
-// seq_dot(q, c, dim) with q in LDS and c in global memory, read 16 bytes at a time
-// when dim % 4 == 0 (rows then 16-byte aligned); the same left-to-right sum.
-__device__ __forceinline__ float exact_dot(const float* __restrict__ q,
-                                           const float* __restrict__ c, int dim) {
-  if ((dim & 3) != 0) return seq_dot(q, c, dim);
-  const float4* c4 = reinterpret_cast<const float4*>(c);
-  const float4* q4 = reinterpret_cast<const float4*>(q);
-  float s = 0.f;
-  int i = 0;
-  for (; i + 4 <= dim / 4; i += 4) {
-    float4 v[4], w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[j] = c4[i + j];
-      w[j] = q4[i + j];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s = s + w[j].x * v[j].x;
-      s = s + w[j].y * v[j].y;
-      s = s + w[j].z * v[j].z;
-      s = s + w[j].w * v[j].w;
-    }
-  }
-  for (; i < dim / 4; ++i) {
-    const float4 v = c4[i], w = q4[i];
-    s = s + w.x * v.x;
-    s = s + w.y * v.y;
-    s = s + w.z * v.z;
-    s = s + w.w * v.w;
-  }
-  return s;
-}
-
 // Score of a 32-bit order key (the inverse of score_key); the NaN key gives +inf.
 __device__ __forceinline__ float key_to_score(uint32_t k) {
   if (k == 0xffffffffu) return __builtin_inff();
@@ -295,7 +261,9 @@ __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
     const int row = kRowsPerWave * wave + rr;
     uint64_t* s = L.slot + row * cap + (f - pre[rr]);
     const uint32_t c = static_cast<uint32_t>(*s);
-    const float dot = exact_dot(L.qs + row * dq, p.centroids + static_cast<int64_t>(c) * dim, dim);
+    const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
+    const float* qrow = L.qs + row * dq;
+    const float dot = (dim & 3) == 0 ? seq_dot_v4(qrow, crow, dim) : seq_dot(qrow, crow, dim);
     *s = make_key((p.qnorm[q0 + row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();

@@ -7,9 +7,12 @@
 // (distance, shortlist rank), flip the sign back for inner product, and pad the
 // remaining slots with (-1, +inf).
 //
-// One wave64 per query: each lane scores shortlist entries i = lane, lane+64, ...
-// with left-to-right fp32 sums, the (key, rank) pairs are sorted in LDS by a
-// single-wave bitonic network, and the first k slots are written.
+// One wave64 per query: the query row is staged in LDS, each lane scores
+// shortlist entries i = lane, lane+64, ... with left-to-right fp32 sums (rows
+// read 16 bytes at a time when dim % 4 == 0), the (key, rank) pairs are sorted in
+// LDS by a single-wave bitonic network, and the first k slots are written. LDS is
+// sized to the shortlist (a power of two >= krefine), so short shortlists keep
+// many waves resident.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -22,17 +25,23 @@ enum { kL2 = 0, kL2Sqrt = 1, kIP = 2, kCosine = 3, kHamming = 4, kLp = 5 };
 // std::max semantics for floats: keeps `a` unless a < b.
 __device__ __forceinline__ float ref_max(float a, float b) { return (a < b) ? b : a; }
 
+// Left-to-right dot product; q (LDS) and x are 16-byte aligned when dim % 4 == 0.
+__device__ __forceinline__ float dot(const float* __restrict__ q, const float* __restrict__ x,
+                                     int dim) {
+  return (dim & 3) == 0 ? seq_dot_v4(q, x, dim) : seq_dot(q, x, dim);
+}
+
 __device__ float metric_value(int metric, const float* __restrict__ q,
                               const float* __restrict__ x, int dim, float qn, float xn) {
   switch (metric) {
     case kL2:
-      return (qn + xn) - 2.f * seq_dot(q, x, dim);
+      return (qn + xn) - 2.f * dot(q, x, dim);
     case kIP:
-      return -seq_dot(q, x, dim);
+      return -dot(q, x, dim);
     case kCosine: {
       // __builtin_sqrtf and '/' lower to correctly rounded sequences (no
       // fast-math, no approximate-sqrt flags), as x86 sqrtss/divss are.
-      const float ip = seq_dot(q, x, dim);
+      const float ip = dot(q, x, dim);
       const float a = __builtin_sqrtf(ref_max(qn, 1e-12f));
       const float b = __builtin_sqrtf(ref_max(xn, 1e-12f));
       return 1.f - ip / (a * b);
@@ -62,12 +71,24 @@ __device__ float metric_value(int metric, const float* __restrict__ q,
   }
 }
 
-__global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a) {
-  __shared__ uint64_t keys[OVVS_HIP_MAX_REFINE];
-  __shared__ float vals[OVVS_HIP_MAX_REFINE];
+constexpr size_t align16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
+
+// LDS: query row [round4(dim)] f32 | keys [M] u64 | vals [M] f32.
+size_t refine_lds(int dim, int M) {
+  return align16(static_cast<size_t>((dim + 3) & ~3) * 4) + static_cast<size_t>(M) * 12;
+}
+
+__global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* qs = reinterpret_cast<float*>(smem);
+  uint64_t* keys =
+      reinterpret_cast<uint64_t*>(smem + align16(static_cast<size_t>((a.dim + 3) & ~3) * 4));
+  float* vals = reinterpret_cast<float*>(keys + Mmax);
   const int64_t q = blockIdx.x;
   const int lane = threadIdx.x;
-  const float* __restrict__ qv = a.queries + q * a.dim;
+  for (int t = lane; t < a.dim; t += 64) qs[t] = a.queries[q * a.dim + t];
+  __syncthreads();
+  const float* __restrict__ qv = qs;
   int cnt = a.short_count[q];
   cnt = cnt < 0 ? 0 : (cnt > a.K ? a.K : cnt);
   int M = 1;
@@ -131,6 +152,16 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
       a.K <= 0 ||
       a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq)), dim3(64), 0, stream, a);
+  int M = 1;
+  while (M < a.K) M <<= 1;
+  const size_t lds = refine_lds(a.dim, M);
+  if (lds > 160u * 1024u) return hipErrorInvalidValue;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_refine),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq)), dim3(64), lds, stream, a, M);
   return hipGetLastError();
 }
