@@ -54,7 +54,7 @@ struct IndexDevice {
   int32_t code_blocks = 0;
   DeviceBuffer centroids;  // [nlist * dim] f32
   DeviceBuffer cnorm;      // [nlist] f32
-  DeviceBuffer cmfma;      // centroids in matrix-core operand order (empty if dim > 128)
+  DeviceBuffer cmfma;      // centroids as split-bf16 matrix-core operands (empty if dim > 128)
   float cnorm_max = 0.f;   // max of cnorm, +inf if any is NaN or inf
   DeviceBuffer codebooks;  // [pq_m * ks * dsub] f32
   DeviceBuffer codes;      // [ceil(n / 64) * code_blocks * 512] u8

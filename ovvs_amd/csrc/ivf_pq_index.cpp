@@ -312,7 +312,7 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
   OVVS_HIP_TRY(ovvs_hip_row_norms(d->dataset.as<float>(), n, static_cast<int32_t>(dim),
                                   d->xnorm.as<float>(), s));
   work.kernel_launches += 2;
-  std::vector<float> cmfma(ovvs_hip_probe_cmfma_floats(static_cast<int32_t>(dim), nlist));
+  std::vector<uint32_t> cmfma(ovvs_hip_probe_cmfma_words(static_cast<int32_t>(dim), nlist));
   if (!cmfma.empty()) {
     ovvs_probe_pack_cmfma(centroids.data(), nlist, static_cast<int32_t>(dim), cmfma.data());
     OVVS_TRY(alloc(d->cmfma, cmfma.size() * 4, work));

@@ -195,7 +195,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       pa.nlist = ix.nlist;
       pa.P = P;
       pa.centroids = dv.centroids.as<float>();
-      pa.cmfma = dv.cmfma.as<float>();
+      pa.cmfma = dv.cmfma.as<uint32_t>();
       pa.cnorm = dv.cnorm.as<float>();
       pa.cnorm_max = dv.cnorm_max;
       pa.probes = d_probes;

@@ -50,11 +50,11 @@ hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nro
 
 // ---- coarse probe on the fp32 matrix cores (probe.hip) ----
 
-// Limits of the fused probe: dim <= 16 * OVVS_PROBE_MAX_DS4 (query fragments held in
-// registers), P <= OVVS_PROBE_MAX_P, at least 2P of its (at most OVVS_PROBE_MAX_GROUPS)
+// Limits of the fused probe: dim <= 32 * OVVS_PROBE_MAX_KSTEPS (query fragments held
+// in registers), P <= OVVS_PROBE_MAX_P, at least 2P of its (at most OVVS_PROBE_MAX_GROUPS)
 // centroid groups, at most 256 (P <= 64) or OVVS_PROBE_CAP exact re-scores per query
 // (a query with more takes the exact route).
-#define OVVS_PROBE_MAX_DS4 8
+#define OVVS_PROBE_MAX_KSTEPS 4
 #define OVVS_PROBE_MAX_P 256
 #define OVVS_PROBE_MAX_GROUPS 512
 #define OVVS_PROBE_CAP 512
@@ -67,7 +67,7 @@ struct OvvsProbeArgs {
   int32_t nlist;
   int32_t P;               // probes per query
   const float* centroids;  // [nlist * dim] row-major (exact re-score)
-  const float* cmfma;      // centroids in matrix-core operand order, see
+  const uint32_t* cmfma;   // centroids as split-bf16 matrix-core operands, see
                            // ovvs_probe_pack_cmfma
   const float* cnorm;      // [nlist], exact row norms
   float cnorm_max;         // max of cnorm (+inf if any is NaN or inf)
@@ -77,12 +77,14 @@ struct OvvsProbeArgs {
 
 // 1 when the fused probe handles these shapes.
 int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t P);
-// Floats in the operand-ordered centroid copy (0 if dim is unsupported).
-size_t ovvs_hip_probe_cmfma_floats(int32_t dim, int32_t nlist);
-// Host-side packing of that copy: for tile t (16 centroids), step group s4 (16
-// dims) and lane l, the float4 at ((t * ceil(dim/16) + s4) * 64 + l) holds, for
-// e = 0..3, C[16t + l%16][16*s4 + 4e + l/16] (zero past nlist or dim).
-void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, float* out);
+// 32-bit words in the split-bf16 centroid operand copy (0 if dim is unsupported).
+size_t ovvs_hip_probe_cmfma_words(int32_t dim, int32_t nlist);
+// Host-side packing of that copy: for tile t (16 centroids), k-step s (32 dims), half
+// h (0: x_hi = bf16(x), 1: x_lo = bf16(x - x_hi), round to nearest even) and lane l,
+// the 16 bytes at word ((((t * ceil(dim/32) + s) * 2 + h) * 64 + l) * 4 hold the 8
+// bf16 values of x = C[16t + l%16][32s + 8(l/16) + j], j = 0..7 (zero past nlist or
+// dim).
+void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, uint32_t* out);
 // Probe selection for every query; flags the queries the exact route must finish.
 hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream);
 // Exact coarse scores S[q*nlist + c] of every centroid, for flagged queries only.

@@ -7,18 +7,25 @@
 // src/prim/mixer.cpp:174-199, src/prim/cpu/cpu_prims.cpp:24-106).
 //
 // k_probe_mfma, one workgroup of kWaves wave64s per 16 queries:
-//   pass 1   v_mfma_f32_16x16x4f32 tiles of 16 queries x 16 centroids give approximate
-//            scores a(q,c). The tiles are cut into nch chunks of gt consecutive tiles;
+//   pass 1   v_mfma_f32_16x16x32_bf16 tiles of 16 queries x 16 centroids give
+//            approximate scores a(q,c) from split operands: every fp32 value x is
+//            x_hi + x_lo with x_hi = bf16(x), x_lo = bf16(x - x_hi) (round to nearest
+//            even; x - x_hi is exact), and q.c ~ q_hi.c_hi + q_hi.c_lo + q_lo.c_hi,
+//            three bf16 products per element accumulated in fp32. The tiles are cut
+//            into nch chunks of gt consecutive tiles;
 //            group (chunk, column j) holds the centroids 16t + j of the chunk's tiles,
 //            and each lane keeps the running minimum of a over its group in registers.
 //            v_q is the P-th smallest of the 16 * nch group minima (as order keys): at
 //            least P distinct centroids (one per group) have a <= t_q, the score v_q
 //            encodes.
-//   bound    E_q >= |a(q,c) - s(q,c)| for every centroid c: both dot products are
-//            fp32 sums of dim products, so each is within gamma_n * |q| * |c|_max of
-//            the real dot product (n = dim + 4, unit roundoff 2^-23 to allow any
-//            rounding mode of the matrix core, plus an absolute term for flushed
-//            subnormals), and the shared |q|^2 + |c|^2 term is rounded once more.
+//   bound    E_q >= |a(q,c) - s(q,c)| for every centroid c. The reference's sequential
+//            dot is within gamma_n |q||c| of the real one (n = dim + 4, u = 2^-23).
+//            The split dot drops q_lo c_lo and the split remainders, at most
+//            3.05 * 2^-16 |q_i c_i| per element, and accumulates 3 * 32 * ksteps exact
+//            bf16 products plus the accumulator in fp32; each addition is allowed 8x
+//            the fp32 unit roundoff (2^-20) whatever order or rounding the matrix
+//            core uses, plus an absolute term for flushed subnormals. The shared
+//            |q|^2 + |c|^2 term is rounded once more in both.
 //   pass 2   every centroid with !(a > T_q), T_q = t_q + 2 E_q rounded up, is a
 //            candidate. A centroid outside has s > t_q + E_q >= s of at least P
 //            candidates, so P entries precede it in the exact order: the exact first
@@ -30,6 +37,8 @@
 // or infinite inputs can cause that), is flagged in `fallback`; k_probe_exact_rows and
 // the flagged row selection of coarse.hip then rank it from exact scores of every
 // centroid.
+#include <cstring>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -38,6 +47,7 @@ using namespace ovvs_dev;
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
@@ -85,24 +95,48 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// bf16 bits of x, rounded to nearest even (NaN stays NaN).
+__host__ __device__ __forceinline__ uint16_t bf16_bits(uint32_t u) {
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// The split of x: hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+  hi = bf16_bits(__float_as_uint(x));
+  const float r = x - __uint_as_float(static_cast<uint32_t>(hi) << 16);
+  lo = bf16_bits(__float_as_uint(r));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 w) {
+  bf16x8 v;
+  __builtin_memcpy(&v, &w, sizeof(v));
+  return v;
+}
+
 // Approximate dot products of tile t: lane holds rows 4*(lane/16)+r, column lane%16.
-// The A operand a[s] = Q[row lane%16][4s + lane/16]; the centroid operand comes from
-// the operand-ordered copy (OvvsProbeArgs::cmfma).
-template <int DS4>
-__device__ __forceinline__ f32x4 tile_dot(const float (&a)[4 * DS4],
-                                          const float* __restrict__ cm, int t) {
+// Operand lane layout of v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][8(l/16)+j]
+// and B[8(l/16)+j][l%16], j = 0..7, per 32-deep k-step. The centroid operands come
+// from the split copy (OvvsProbeArgs::cmfma): per tile and k-step, 64 lanes x 16 B
+// of high parts, then 64 lanes x 16 B of low parts.
+template <int KS>
+__device__ __forceinline__ f32x4 tile_dot(const bf16x8 (&ah)[KS], const bf16x8 (&al)[KS],
+                                          const uint32_t* __restrict__ cm, int t) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const float4* src =
-      reinterpret_cast<const float4*>(cm) + static_cast<int64_t>(t) * DS4 * 64 + lane_id();
-  float4 b[DS4];
+  const uint4* src =
+      reinterpret_cast<const uint4*>(cm) + static_cast<int64_t>(t) * KS * 2 * 64 + lane_id();
+  uint4 bh[KS], bl[KS];
 #pragma unroll
-  for (int s4 = 0; s4 < DS4; ++s4) b[s4] = src[s4 * 64];
+  for (int s = 0; s < KS; ++s) {
+    bh[s] = src[(2 * s) * 64];
+    bl[s] = src[(2 * s + 1) * 64];
+  }
 #pragma unroll
-  for (int s4 = 0; s4 < DS4; ++s4) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 0], b[s4].x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 1], b[s4].y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 2], b[s4].z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4 + 3], b[s4].w, acc, 0, 0, 0);
+  for (int s = 0; s < KS; ++s) {
+    const bf16x8 h = as_bf16x8(bh[s]), l = as_bf16x8(bl[s]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[s], h, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[s], l, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[s], h, acc, 0, 0, 0);
   }
   return acc;
 }
@@ -121,23 +155,28 @@ __device__ __forceinline__ float next_up(float f) {
 }
 
 // Candidate bound T = t + 2E for one query (see the file comment), rounded up.
-__device__ float candidate_bound(float t, float qn, float cn_max, int dim) {
+__device__ float candidate_bound(float t, float qn, float cn_max, int dim, int ksteps) {
   if (!(t < __builtin_inff()) || !(qn < __builtin_inff()) || !(cn_max < __builtin_inff()))
     return __builtin_inff();
-  const double u = 1.1920928955078125e-7;  // 2^-23
+  const double u = 1.1920928955078125e-7;   // 2^-23
+  const double um = 9.5367431640625e-7;     // 2^-20, per matrix-core addition
   const double n = static_cast<double>(dim) + 4.0;
   const double gamma = n * u / (1.0 - n * u);
+  const double m = 3.0 * 32.0 * ksteps + 3.0 * ksteps + 16.0;
+  const double gm = m * um / (1.0 - m * um);
+  const double emf = 3.05 * 1.52587890625e-5 + 1.02 * gm;  // 2^-16 split remainder
   const double qd = static_cast<double>(qn) * (1.0 + 4.0 * n * u);
   const double cd = static_cast<double>(cn_max) * (1.0 + 4.0 * n * u);
   const double S = sqrt(qd * cd) * (1.0 + 1e-6);
-  const double E = 2.0 * (4.0 * gamma * S + 2.0 * u * (qd + cd + 2.0 * S)) + n * 1e-30;
+  const double E = 2.0 * (2.0 * (emf + gamma) * S + 2.0 * u * (qd + cd + 2.0 * S)) +
+                   m * 1e-30 * (1.0 + sqrt(qd) + sqrt(cd));
   const double T = static_cast<double>(t) + 2.0 * E;
   float f = static_cast<float>(T);
   if (static_cast<double>(f) < T && f < __builtin_inff()) f = next_up(f);
   return f;
 }
 
-template <int DS4>
+template <int KS>
 __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
                                                          const ProbeShape shape) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -156,11 +195,17 @@ __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
   if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
   __syncthreads();
 
-  float a[4 * DS4];
+  bf16x8 ah[KS], al[KS];
 #pragma unroll
-  for (int s = 0; s < 4 * DS4; ++s) {
-    const int k = 4 * s + (lane >> 4);
-    a[s] = k < dim ? L.qs[(lane & 15) * dq + k] : 0.f;
+  for (int s = 0; s < KS; ++s) {
+    uint16_t h[8], l[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = 32 * s + 8 * (lane >> 4) + j;
+      split_bf16(k < dim ? L.qs[(lane & 15) * dq + k] : 0.f, h[j], l[j]);
+    }
+    __builtin_memcpy(&ah[s], h, sizeof(h));
+    __builtin_memcpy(&al[s], l, sizeof(l));
   }
   float qn[4];
 #pragma unroll
@@ -176,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
     const int t1 = min(t0 + shape.gt, shape.ntile);
     float m[4] = {__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff()};
     for (int t = t0; t < t1; ++t) {
-      const f32x4 acc = tile_dot<DS4>(a, p.cmfma, t);
+      const f32x4 acc = tile_dot<KS>(ah, al, p.cmfma, t);
       const int c = 16 * t + col;
       if (c < p.nlist) {
         const float cn = p.cnorm[c];
@@ -212,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
     if (lane == 0) {
       const int64_t q = q0 + row;
       const float qnr = q < p.nq ? p.qnorm[q] : 0.f;
-      L.thr[row] = candidate_bound(key_to_score(v), qnr, p.cnorm_max, dim);
+      L.thr[row] = candidate_bound(key_to_score(v), qnr, p.cnorm_max, dim, KS);
     }
   }
   __syncthreads();
@@ -223,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
   for (int r = 0; r < 4; ++r) T[r] = L.thr[4 * (lane >> 4) + r];
   const int cap = shape.cap;
   for (int t = wave; t < shape.ntile; t += kWaves) {
-    const f32x4 acc = tile_dot<DS4>(a, p.cmfma, t);
+    const f32x4 acc = tile_dot<KS>(ah, al, p.cmfma, t);
     const int c = 16 * t + col;
     if (c < p.nlist) {
       const float cn = p.cnorm[c];
@@ -297,7 +342,7 @@ __global__ __launch_bounds__(256) void k_probe_exact_rows(
 
 // Shape of a launch, or false when the fused probe does not serve these sizes.
 bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
-  if (dim <= 0 || dim > 16 * OVVS_PROBE_MAX_DS4 || nlist <= 0 || nlist > (1 << 24) || P <= 0 ||
+  if (dim <= 0 || dim > 32 * OVVS_PROBE_MAX_KSTEPS || nlist <= 0 || nlist > (1 << 24) || P <= 0 ||
       P > OVVS_PROBE_MAX_P)
     return false;
   sh->ntile = (nlist + 15) / 16;
@@ -317,16 +362,16 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
   return sh->lds <= 160 * 1024;
 }
 
-template <int DS4>
+template <int KS>
 hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
   if (sh.lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<DS4>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<KS>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(sh.lds));
     if (e != hipSuccess) return e;
   }
   const int64_t blocks = (p.nq + kRows - 1) / kRows;
-  hipLaunchKernelGGL(k_probe_mfma<DS4>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads),
+  hipLaunchKernelGGL(k_probe_mfma<KS>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads),
                      sh.lds, stream, p, sh);
   return hipGetLastError();
 }
@@ -338,21 +383,39 @@ extern "C" int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t
   return probe_shape(dim, nlist, P, &sh) ? 1 : 0;
 }
 
-extern "C" size_t ovvs_hip_probe_cmfma_floats(int32_t dim, int32_t nlist) {
-  if (dim <= 0 || dim > 16 * OVVS_PROBE_MAX_DS4 || nlist <= 0) return 0;
-  return static_cast<size_t>((nlist + 15) / 16) * 16 * (16 * ((dim + 15) / 16));
+extern "C" size_t ovvs_hip_probe_cmfma_words(int32_t dim, int32_t nlist) {
+  if (dim <= 0 || dim > 32 * OVVS_PROBE_MAX_KSTEPS || nlist <= 0) return 0;
+  const size_t ks = static_cast<size_t>((dim + 31) / 32);
+  return static_cast<size_t>((nlist + 15) / 16) * ks * 2 * 64 * 4;
 }
 
-extern "C" void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, float* out) {
-  const int ds4 = (dim + 15) / 16, ntile = (nlist + 15) / 16;
+extern "C" void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim,
+                                      uint32_t* out) {
+  const int ks = (dim + 31) / 32, ntile = (nlist + 15) / 16;
   for (int t = 0; t < ntile; ++t)
-    for (int s4 = 0; s4 < ds4; ++s4)
-      for (int lane = 0; lane < 64; ++lane)
-        for (int e = 0; e < 4; ++e) {
-          const int s = 4 * s4 + e, k = 4 * s + lane / 16, c = 16 * t + lane % 16;
-          out[((static_cast<size_t>(t) * ds4 + s4) * 64 + lane) * 4 + e] =
-              (c < nlist && k < dim) ? C[static_cast<size_t>(c) * dim + k] : 0.f;
+    for (int s = 0; s < ks; ++s)
+      for (int lane = 0; lane < 64; ++lane) {
+        uint16_t hi[8], lo[8];
+        for (int j = 0; j < 8; ++j) {
+          const int k = 32 * s + 8 * (lane / 16) + j, c = 16 * t + lane % 16;
+          const float x = (c < nlist && k < dim) ? C[static_cast<size_t>(c) * dim + k] : 0.f;
+          uint32_t u;
+          std::memcpy(&u, &x, 4);
+          hi[j] = bf16_bits(u);
+          const uint32_t hu = static_cast<uint32_t>(hi[j]) << 16;
+          float h;
+          std::memcpy(&h, &hu, 4);
+          const float r = x - h;
+          std::memcpy(&u, &r, 4);
+          lo[j] = bf16_bits(u);
         }
+        uint32_t* dh = out + ((static_cast<size_t>(t) * ks + s) * 2 * 64 + lane) * 4;
+        uint32_t* dl = dh + 64 * 4;
+        for (int w = 0; w < 4; ++w) {
+          dh[w] = static_cast<uint32_t>(hi[2 * w]) | (static_cast<uint32_t>(hi[2 * w + 1]) << 16);
+          dl[w] = static_cast<uint32_t>(lo[2 * w]) | (static_cast<uint32_t>(lo[2 * w + 1]) << 16);
+        }
+      }
 }
 
 extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream) {
@@ -363,15 +426,11 @@ extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t
   if (!p.queries || !p.qnorm || !p.centroids || !p.cmfma || !p.cnorm || !p.probes ||
       !p.fallback || p.nq > 0x7fffffff || !probe_shape(p.dim, p.nlist, p.P, &sh))
     return hipErrorInvalidValue;
-  switch ((p.dim + 15) / 16) {
+  switch ((p.dim + 31) / 32) {
     case 1: return launch_probe<1>(p, sh, stream);
     case 2: return launch_probe<2>(p, sh, stream);
     case 3: return launch_probe<3>(p, sh, stream);
-    case 4: return launch_probe<4>(p, sh, stream);
-    case 5: return launch_probe<5>(p, sh, stream);
-    case 6: return launch_probe<6>(p, sh, stream);
-    case 7: return launch_probe<7>(p, sh, stream);
-    default: return launch_probe<8>(p, sh, stream);
+    default: return launch_probe<4>(p, sh, stream);
   }
 }
 
