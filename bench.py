@@ -163,6 +163,55 @@ def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample, thr
     return base, parity
 
 
+def _fill_rows(shm_name, shape, cfg, C, a, b):
+    from multiprocessing import shared_memory
+
+    from ovvs_amd import synth
+
+    shm = shared_memory.SharedMemory(name=shm_name)
+    out = np.ndarray(shape, dtype=np.float32, buffer=shm.buf)
+    for s in range(a, b, 65536):
+        e = min(b, s + 65536)
+        out[s:e] = synth.base_rows(cfg, s, e - s, C)
+    del out
+    shm.close()
+
+
+def generate_base(cfg, C, workers):
+    """The config's base rows. Large configs are generated by `workers` forked
+    processes into shared memory (each row is a pure function of its index, so
+    the result is the same as the single-process generator); returns the array and
+    the shared-memory handle to release (None for the in-process path)."""
+    from ovvs_amd import synth
+
+    nbytes = cfg.n * cfg.dim * 4
+    if nbytes < (2 << 30) or workers <= 1:
+        return synth.base_rows(cfg, 0, cfg.n, C), None
+    from multiprocessing import get_context, shared_memory
+
+    shm = shared_memory.SharedMemory(create=True, size=nbytes)
+    shape = (cfg.n, cfg.dim)
+    bounds = np.linspace(0, cfg.n, 4 * workers + 1).astype(np.int64)
+    ctx = get_context("fork")
+    pending = [(int(bounds[i]), int(bounds[i + 1])) for i in range(len(bounds) - 1)]
+    running = []
+    while pending or running:
+        while pending and len(running) < workers:
+            a, b = pending.pop(0)
+            pr = ctx.Process(target=_fill_rows, args=(shm.name, shape, cfg, C, a, b))
+            pr.start()
+            running.append(pr)
+        pr = running.pop(0)
+        pr.join()
+        if pr.exitcode != 0:
+            shm.close()
+            shm.unlink()
+            raise RuntimeError("base row generation failed")
+        log(f"generated rows: {len(bounds) - 1 - len(pending) - len(running)}/{len(bounds) - 1} "
+            f"slices")
+    return np.ndarray(shape, dtype=np.float32, buffer=shm.buf), shm
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,11 +219,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--nq", type=int, default=None, help="query batch (default: config's)")
+    ap.add_argument("--rows", type=int, default=None,
+                    help="base rows (default: config's; a prefix of its stream)")
     ap.add_argument("--krefine", type=int, default=None, help="default: k")
     ap.add_argument("--cpu-sample", type=int, default=1000,
                     help="queries of the single-thread reference timing")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
                     help="threads of the whole-batch reference timing")
+    ap.add_argument("--gen-workers", type=int, default=min(16, os.cpu_count() or 1),
+                    help="processes generating the base rows of large configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -194,6 +247,10 @@ def main() -> int:
     from ovvs_amd import synth
 
     cfg = synth.CONFIGS[args.config]
+    if args.rows:
+        import dataclasses
+
+        cfg = dataclasses.replace(cfg, n=args.rows, train_rows=min(cfg.train_rows, args.rows))
     nq = args.nq or cfg.nq
     k = cfg.k
     krefine = args.krefine or k
@@ -201,9 +258,20 @@ def main() -> int:
     log(f"config {cfg.name}: n={cfg.n} dim={cfg.dim} nlist={cfg.nlist} pq_m={cfg.pq_m} "
         f"nprobe={cfg.nprobe} k={k} krefine={krefine} nq={nq}")
     C = synth.centers(cfg)
-    base = synth.base_rows(cfg, 0, cfg.n, C)
+    # Forked generator processes: no HIP runtime has been initialised yet.
+    base, shm = generate_base(cfg, C, args.gen_workers)
     queries = synth.query_rows(cfg, 0, nq, C)
     log("data generated")
+    try:
+        return run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries)
+    finally:
+        if shm is not None:
+            del base
+            shm.close()
+            shm.unlink()
+
+
+def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
 
     res = ovvs_amd.Resources()
     t = time.perf_counter()

@@ -467,14 +467,21 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         // addresses held in registers across it.
         uint32_t loff_b = loff;
         asm volatile("" : "+v"(loff_b));
-        uint2 w_next = make_uint2(0u, 0u);
-        if (__builtin_amdgcn_inverse_ballot_w64(live[0]))
-          w_next = *reinterpret_cast<const uint2*>(bbase + loff_b);
+        // Every live row's code word of this block is requested up front (codes
+        // that are not L2-resident cost an HBM round trip each).
+        constexpr int kD = kRowsPerLane;
+        uint2 wq[kD];
+#pragma unroll
+        for (int d = 0; d < kD; ++d) {
+          wq[d] = make_uint2(0u, 0u);
+          if (d < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[d]))
+            wq[d] = *reinterpret_cast<const uint2*>(bbase + (loff_b + d * row_step));
+        }
 #pragma unroll
         for (int i = 0; i < kRowsPerLane; ++i) {
-          const uint2 w = w_next;
-          if (i + 1 < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[i + 1]))
-            w_next = *reinterpret_cast<const uint2*>(bbase + (loff_b + (i + 1) * row_step));
+          const uint2 w = wq[i % kD];
+          if (i + kD < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[i + kD]))
+            wq[i % kD] = *reinterpret_cast<const uint2*>(bbase + (loff_b + (i + kD) * row_step));
           // Uniform skip; within a live row every lane scores its code word (a
           // dead lane's word is an earlier row's or zero, so its table reads stay
           // in the slice) and only live lanes keep the result.
