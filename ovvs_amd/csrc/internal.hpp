@@ -46,20 +46,53 @@ class DeviceBuffer {
   size_t bytes_ = 0;
 };
 
-// Device copy of an index. Codes are list-major in the tiled block layout of
-// kernels.hpp (OVVS_CODE_TILE_ROWS); ids are list-major; offsets are the list
-// CSR; dataset rows are by id.
+// Host form of the scan order (scan_layout.cpp): each list's rows split into
+// segments of rows with nearby reconstructions, every segment starting at a
+// 64-row code tile (the tail of its last tile is padding).
+struct ScanLayoutHost {
+  int64_t positions = 0;           // scan positions: rows plus padding, a multiple of 64
+  int32_t box_dims = 0;            // pq_m * dsub
+  std::vector<int32_t> list_seg;   // [nlist + 1] segment CSR
+  std::vector<int32_t> seg_start;  // [nseg] first scan position
+  std::vector<int32_t> seg_len;    // [nseg] rows
+  std::vector<uint32_t> seg_box;   // [nseg * box_dims] (lo, hi) of the reconstructions, as
+                                   // binary16 rounded outward, packed lo | hi << 16
+  std::vector<uint32_t> list_box;  // [nlist * box_dims] the same over each whole list
+  std::vector<int64_t> ids;        // [positions] row id, -1 for padding
+  std::vector<int32_t> rord;       // [positions] index of the row within its list, -1 padding
+  std::vector<uint8_t> codes;      // tiled codes by scan position (kernels.hpp)
+};
+
+// Segments of at most seg_rows rows. Fails with DEVICE_UNAVAILABLE when the scan
+// positions or segments exceed 32-bit indexing.
+ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayoutHost& out);
+// Largest binary16 <= lo and smallest >= hi, packed lo | hi << 16 (lo, hi not NaN),
+// and the inverse of one half of it.
+uint32_t pack_box_fp16(float lo, float hi);
+float unpack_box_fp16(uint32_t b, int hi);
+
+// Device copy of an index. Codes, ids and in-list row indices are in scan order
+// (ScanLayoutHost); offsets are the reference's list CSR (rows per list and the
+// ordinal base of each list); dataset rows are by id.
 struct IndexDevice {
   int device = -1;
   int32_t code_blocks = 0;
+  int64_t positions = 0;   // scan positions
+  int32_t box_dims = 0;    // dimensions of each segment box (0: no boxes)
   DeviceBuffer centroids;  // [nlist * dim] f32
   DeviceBuffer cnorm;      // [nlist] f32
   DeviceBuffer cmfma;      // centroids as split-bf16 matrix-core operands (empty if dim > 128)
   float cnorm_max = 0.f;   // max of cnorm, +inf if any is NaN or inf
   DeviceBuffer codebooks;  // [pq_m * ks * dsub] f32
-  DeviceBuffer codes;      // [ceil(n / 64) * code_blocks * 512] u8
-  DeviceBuffer ids;        // [n] i64
+  DeviceBuffer codes;      // [positions / 64 * code_blocks * 512] u8
+  DeviceBuffer ids;        // [positions] i64
+  DeviceBuffer rord;       // [positions] i32
   DeviceBuffer offsets;    // [nlist + 1] i64
+  DeviceBuffer list_seg;   // [nlist + 1] i32
+  DeviceBuffer seg_start;  // [nseg] i32
+  DeviceBuffer seg_len;    // [nseg] i32
+  DeviceBuffer seg_box;    // [nseg * box_dims] packed binary16 (lo, hi)
+  DeviceBuffer list_box;   // [nlist * box_dims] packed binary16 (lo, hi)
   DeviceBuffer dataset;    // [n * dim] f32
   DeviceBuffer xnorm;      // [n] f32
 };

@@ -272,40 +272,50 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
   if (!ovvs::lists_valid(*this)) return OVVS_STATUS_ERROR;
   auto d = std::make_unique<ovvs::IndexDevice>();
   d->device = res.device;
-  constexpr size_t kB = OVVS_CODE_BLOCK, kT = OVVS_CODE_TILE_ROWS;
-  const size_t nblocks = (static_cast<size_t>(pq_m) + kB - 1) / kB;
-  d->code_blocks = static_cast<int32_t>(nblocks);
-  const size_t tiles = (static_cast<size_t>(n) + kT - 1) / kT;
+  constexpr size_t kB = OVVS_CODE_BLOCK;
+  d->code_blocks = static_cast<int32_t>((static_cast<size_t>(pq_m) + kB - 1) / kB);
   std::vector<int64_t> offsets(static_cast<size_t>(nlist) + 1, 0);
-  std::vector<int64_t> ids(static_cast<size_t>(n));
-  std::vector<uint8_t> packed(tiles * nblocks * kT * kB, 0);
-  size_t pos = 0;
   for (int32_t c = 0; c < nlist; ++c) {
-    for (const int64_t id : lists[static_cast<size_t>(c)]) {
-      ids[pos] = id;
-      const uint8_t* src = codes.data() + static_cast<size_t>(id) * pq_m;
-      uint8_t* tile = packed.data() + (pos / kT) * (nblocks * kT * kB) + (pos % kT) * kB;
-      for (size_t m = 0; m < static_cast<size_t>(pq_m); ++m) {
-        tile[(m / kB) * (kT * kB) + (m % kB)] = src[m];
-      }
-      ++pos;
-    }
-    offsets[static_cast<size_t>(c) + 1] = static_cast<int64_t>(pos);
+    offsets[static_cast<size_t>(c) + 1] =
+        offsets[static_cast<size_t>(c)] + static_cast<int64_t>(lists[static_cast<size_t>(c)].size());
   }
+  ovvs::ScanLayoutHost lay;
+  OVVS_TRY(ovvs::make_scan_layout(*this, OVVS_SEGMENT_ROWS, lay));
+  d->positions = lay.positions;
+  // The scan's bound arithmetic covers boxes of up to OVVS_MAX_BOX_DIMS dimensions.
+  d->box_dims = lay.box_dims <= OVVS_MAX_BOX_DIMS ? lay.box_dims : 0;
+  const size_t nseg = lay.seg_start.size();
   hipStream_t s = res.stream;
   OVVS_TRY(alloc(d->centroids, centroids.size() * 4, work));
   OVVS_TRY(alloc(d->cnorm, static_cast<size_t>(nlist) * 4, work));
   OVVS_TRY(alloc(d->codebooks, codebooks.size() * 4, work));
-  OVVS_TRY(alloc(d->codes, packed.size(), work));
-  OVVS_TRY(alloc(d->ids, ids.size() * 8, work));
+  OVVS_TRY(alloc(d->codes, lay.codes.size(), work));
+  OVVS_TRY(alloc(d->ids, lay.ids.size() * 8, work));
+  OVVS_TRY(alloc(d->rord, lay.rord.size() * 4, work));
   OVVS_TRY(alloc(d->offsets, offsets.size() * 8, work));
+  OVVS_TRY(alloc(d->list_seg, lay.list_seg.size() * 4, work));
+  OVVS_TRY(alloc(d->seg_start, std::max<size_t>(nseg, 1) * 4, work));
+  OVVS_TRY(alloc(d->seg_len, std::max<size_t>(nseg, 1) * 4, work));
+  if (d->box_dims > 0) {
+    OVVS_TRY(alloc(d->seg_box, std::max<size_t>(lay.seg_box.size(), 1) * 4, work));
+    OVVS_TRY(alloc(d->list_box, lay.list_box.size() * 4, work));
+    OVVS_TRY(h2d(d->list_box.get(), lay.list_box.data(), lay.list_box.size() * 4, s, work));
+  }
   OVVS_TRY(alloc(d->dataset, dataset.size() * 4, work));
   OVVS_TRY(alloc(d->xnorm, static_cast<size_t>(n) * 4, work));
   OVVS_TRY(h2d(d->centroids.get(), centroids.data(), centroids.size() * 4, s, work));
   OVVS_TRY(h2d(d->codebooks.get(), codebooks.data(), codebooks.size() * 4, s, work));
-  OVVS_TRY(h2d(d->codes.get(), packed.data(), packed.size(), s, work));
-  OVVS_TRY(h2d(d->ids.get(), ids.data(), ids.size() * 8, s, work));
+  OVVS_TRY(h2d(d->codes.get(), lay.codes.data(), lay.codes.size(), s, work));
+  OVVS_TRY(h2d(d->ids.get(), lay.ids.data(), lay.ids.size() * 8, s, work));
+  OVVS_TRY(h2d(d->rord.get(), lay.rord.data(), lay.rord.size() * 4, s, work));
   OVVS_TRY(h2d(d->offsets.get(), offsets.data(), offsets.size() * 8, s, work));
+  OVVS_TRY(h2d(d->list_seg.get(), lay.list_seg.data(), lay.list_seg.size() * 4, s, work));
+  if (nseg > 0) {
+    OVVS_TRY(h2d(d->seg_start.get(), lay.seg_start.data(), nseg * 4, s, work));
+    OVVS_TRY(h2d(d->seg_len.get(), lay.seg_len.data(), nseg * 4, s, work));
+    if (d->box_dims > 0)
+      OVVS_TRY(h2d(d->seg_box.get(), lay.seg_box.data(), lay.seg_box.size() * 4, s, work));
+  }
   OVVS_TRY(h2d(d->dataset.get(), dataset.data(), dataset.size() * 4, s, work));
   OVVS_HIP_TRY(ovvs_hip_row_norms(d->centroids.as<float>(), nlist, static_cast<int32_t>(dim),
                                   d->cnorm.as<float>(), s));

@@ -114,7 +114,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
   // for krefine > 128 (indexes.cpp:576-584).
   // OVVS_HIP_MAX_REFINE bounds krefine and k.
   if (R > OVVS_HIP_MAX_REFINE || P > OVVS_HIP_MAX_PROBES ||
-      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16, R) == 0 ||
+      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16, R, P) == 0 ||
       nq > 0x7fffffff || ix.n > 0x7fffffff) {
     return OVVS_STATUS_DEVICE_UNAVAILABLE;
   }
@@ -240,8 +240,15 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.code_blocks = dv.code_blocks;
     sa.nlist = ix.nlist;
     sa.list_offsets = dv.offsets.as<int64_t>();
+    sa.list_seg = dv.list_seg.as<int32_t>();
+    sa.seg_start = dv.seg_start.as<int32_t>();
+    sa.seg_len = dv.seg_len.as<int32_t>();
+    sa.seg_box = dv.box_dims > 0 ? dv.seg_box.as<uint32_t>() : nullptr;
+    sa.list_box = dv.box_dims > 0 ? dv.list_box.as<uint32_t>() : nullptr;
+    sa.positions = dv.positions;
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();
+    sa.rord = dv.rord.as<int32_t>();
     sa.bitset = d_bitset;
     sa.K = R;
     sa.lut_f16 = lut_f16;
@@ -261,6 +268,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.dataset = dv.dataset.as<float>();
     ra.xnorm = dv.xnorm.as<float>();
     ra.n = ix.n;
+    ra.positions = dv.positions;
     ra.ids = dv.ids.as<int64_t>();
     ra.K = R;
     ra.short_pos = d_spos;

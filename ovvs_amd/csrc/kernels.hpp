@@ -28,6 +28,16 @@ extern "C" {
 #define OVVS_CODE_BLOCK 8
 #define OVVS_CODE_TILE_ROWS 64
 
+// Scan order of the device mirror: each list's rows are split into segments of
+// at most OVVS_SEGMENT_ROWS rows with nearby PQ reconstructions; a segment
+// starts at a code tile and carries the (lo, hi) range of its rows'
+// reconstructions in every subspace dimension (its box). Rows keep their
+// index within the list, which is what orders candidates.
+#define OVVS_SEGMENT_ROWS 128
+// Boxes are used when pq_m * dsub is at most this (the scan's rounding-error
+// allowance for its lower bounds holds up to there).
+#define OVVS_MAX_BOX_DIMS 2048
+
 // out[i] = sum_t x[i*dim+t]^2, left to right from +0 (reference internal.hpp:221-225).
 hipError_t ovvs_hip_row_norms(const float* x, int64_t n, int32_t dim, float* out,
                               hipStream_t stream);
@@ -111,14 +121,22 @@ struct OvvsScanArgs {
   int32_t dsub;
   int32_t code_blocks;         // ceil(pq_m / OVVS_CODE_BLOCK)
   int32_t nlist;
-  const int64_t* list_offsets; // [nlist + 1]
-  const uint8_t* codes;        // tiled list-major codes, see OVVS_CODE_TILE_ROWS
-  const int64_t* ids;          // [n], list-major
+  const int64_t* list_offsets; // [nlist + 1] the reference's list CSR (rows per list)
+  const int32_t* list_seg;     // [nlist + 1] segment CSR
+  const int32_t* seg_start;    // [nseg] first scan position of each segment (tile aligned)
+  const int32_t* seg_len;      // [nseg] rows of each segment
+  const uint32_t* seg_box;     // [nseg * pq_m * dsub] (lo, hi) per dimension as binary16
+                               // rounded outward, packed lo | hi << 16; or nullptr
+  const uint32_t* list_box;    // [nlist * pq_m * dsub] the same over each list; or nullptr
+  int64_t positions;           // scan positions
+  const uint8_t* codes;        // tiled codes by scan position, see OVVS_CODE_TILE_ROWS
+  const int64_t* ids;          // [positions] row ids by scan position
+  const int32_t* rord;         // [positions] index of each row within its list
   const uint8_t* bitset;       // (n+7)/8 bytes or nullptr
   int32_t K;                   // shortlist length (krefine), 1..OVVS_HIP_MAX_REFINE
   int32_t lut_f16;             // 0: fp32 table entries, 1: binary16 entries
   uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
-  int32_t* out_pos;            // [nq * K] packed positions
+  int32_t* out_pos;            // [nq * K] scan positions
   int32_t* out_count;          // [nq]
   unsigned long long* counters; // [4]: += scanned rows, += non-empty (query, list) tasks,
                                 //      += shortlist entries, += probe ids out of range
@@ -127,9 +145,10 @@ struct OvvsScanArgs {
 // Fused residual-LUT build (in LDS) + ADC code scan + per-query shortlist of
 // the K best (ADC score, dense ordinal) rows over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
-// Dynamic LDS bytes the scan kernel needs for these shapes and shortlist
-// length (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
-size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K);
+// Dynamic LDS bytes the scan kernel needs for these shapes, shortlist length and
+// probe count (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
+size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K,
+                               int32_t P);
 
 struct OvvsRefineArgs {
   const float* queries;   // [nq * dim]
@@ -140,7 +159,8 @@ struct OvvsRefineArgs {
   const float* dataset;   // [n * dim], row = id
   const float* xnorm;     // [n]
   int64_t n;
-  const int64_t* ids;     // [n] list-major (packed position -> id)
+  int64_t positions;      // entries of ids
+  const int64_t* ids;     // [positions] scan position -> id
   int32_t K;              // shortlist stride
   const int32_t* short_pos;    // [nq * K]
   const int32_t* short_count;  // [nq]

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax)
       // Positions come from the scan; one out of range is reported (the search
       // then fails) instead of being dereferenced.
       const int32_t pos = a.short_pos[q * a.K + i];
-      const int64_t id = (pos >= 0 && pos < a.n) ? a.ids[pos] : -1;
+      const int64_t id = (pos >= 0 && pos < a.positions) ? a.ids[pos] : -1;
       if (id >= 0 && id < a.n) {
         const float v = metric_value(a.metric, qv, a.dataset + id * a.dim, a.dim, a.qnorm[q],
                                      a.xnorm[id]);
@@ -148,7 +148,8 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
   const OvvsRefineArgs& a = *args;
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.qnorm || !a.dataset || !a.xnorm || !a.ids || !a.short_pos ||
-      !a.short_count || !a.out_ids || !a.out_dist || !a.invalid || a.n <= 0 || a.dim <= 0 ||
+      !a.short_count || !a.out_ids || !a.out_dist || !a.invalid || a.n <= 0 || a.positions <= 0 ||
+      a.dim <= 0 ||
       a.K <= 0 ||
       a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff)
     return hipErrorInvalidValue;

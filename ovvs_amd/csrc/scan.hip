@@ -1,5 +1,4 @@
-// scan.hip — fused residual-LUT build + PQ code scan + shortlist select for
-// IVF-PQ search on gfx950.
+// scan.hip — fused code scan + shortlist select for IVF-PQ search on gfx950.
 //
 // Reference behaviour: for every probed list l of query q (in probe-rank order)
 // the residual r = q - c_l gives the table T[m][j] = sum_u (r[m*dsub+u] -
@@ -10,29 +9,37 @@
 // order (indexes.cpp:683-712,1019-1066; the reference's own GPU design for this
 // step is src/prim/gpu/backend_gpu.cpp:791-1010).
 //
-// Design (one 256-lane workgroup per query, four wave64s):
-//   * Rows are processed in chunks of up to 2048 (8 per lane, partial sums in
-//     registers) and subspaces in blocks of 8. For each block the workgroup
-//     builds only that block's 8 x ks table slice into LDS (each entry with the
-//     reference's operation order), then every live row adds its 8 entries in
-//     order m = 8b..8b+7.
-//   * Table entries are squared distances (>= +0, or NaN), so fp32 partial sums
-//     never decrease. A row whose partial sum already exceeds the K-th best key
-//     of any wave (each such key has K better rows behind it) cannot enter the
-//     shortlist and is dropped; when a block has no live row left the remaining
-//     blocks (their table slices and their code bytes) are skipped. Surviving
-//     rows are scored completely, so the shortlist is exactly the reference's.
-//   * Codes are stored tiled: 64-row tiles, inside a tile 8-byte slabs of one
-//     block for 64 consecutive rows, so a wave's block load is one coalesced
-//     512-byte access and skipped blocks are never fetched.
+// Design (one 256-lane workgroup per query; its four wave64s work independently,
+// wave w on the probed lists of rank w, w+4, ..., and share only the K-th best
+// keys they publish in LDS):
+//   * The device mirror stores each list as segments of up to 128 rows with
+//     nearby PQ reconstructions, each with the per-dimension range (box) of its
+//     rows' reconstructions. For the residual r, the entry of subspace m of any
+//     row of the segment is at least the sum over m's dimensions of the squared
+//     distance from r to the box, so the box bounds every row's score from below
+//     (and the part after block 0). fp32 rounding is monotone, so the bounds hold
+//     for the rounded scores up to a small relative allowance.
+//   * A segment whose bound exceeds the K-th best score found so far cannot
+//     contribute: it is skipped without reading its codes. Segment bounds are
+//     evaluated 4-64 lanes per segment, up to 16 segments per pass.
+//   * Rows of the other segments are read in 64-row code tiles (one coalesced
+//     512-byte access per wave and block) and scored through block 0 (the first 8
+//     subspaces). A row whose partial sum plus the segment's tail bound still
+//     exceeds the K-th best is dropped; the rest are queued and, 64 at a time,
+//     completed block by block. Table entries are computed where they are used,
+//     from the codebook, with the reference's operation order: with the bounds in
+//     place a query scores a few hundred rows, so building whole tables would cost
+//     more than the entries it reads. Every row that can enter the shortlist is
+//     scored completely, so the shortlist is exactly the reference's.
 //   * Each wave keeps its own running top-K as a sorted register list (64 keys
 //     per register row, KPL rows), a 128-slot LDS candidate buffer and a
 //     threshold it publishes in LDS: rows are appended with ballot/popcount (no
 //     atomics), buffers are merged by a cross-lane bitonic sort plus a bitonic
 //     merge, and at the end the four lists are merged once.
-// Keys are (order-preserving score bits << 32 | raw ordinal); raw ordinals count
-// every row of earlier probed lists, which orders accepted rows exactly as the
-// dense ordinal does.
+// Keys are (order-preserving score bits << 32 | raw ordinal); a row's raw ordinal
+// is the number of rows of earlier probed lists plus its index within its list,
+// which orders accepted rows exactly as the dense ordinal does, whatever order the
+// scan visits them in.
 #include <hip/hip_fp16.h>
 
 #include "device_common.hpp"
@@ -45,8 +52,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kBufCap = 128;
-constexpr int kRowsPerLane = 8;
-constexpr int kChunkRows = kThreads * kRowsPerLane;
 constexpr int kBlock = OVVS_CODE_BLOCK;      // subspaces per block (8)
 constexpr int kTile = OVVS_CODE_TILE_ROWS;   // rows per code tile (64)
 
@@ -200,146 +205,214 @@ struct Codeword {
   }
 };
 
-// build_slice for ks == 256: thread j computes entry (i, j) of every subspace i of
-// the slice; codebook loads are issued a group of subspaces (16 floats) at a time
-// ahead of the arithmetic.
-template <int DSUB, bool F16>
-__device__ __forceinline__ void build_slice_256(const float* resid,
-                                                const float* __restrict__ codebooks, int m0,
-                                                int mb, float* lut32, uint16_t* lut16) {
-  constexpr int kGroup = DSUB <= 2 ? kBlock : 16 / DSUB;
-  const int j = static_cast<int>(threadIdx.x);
-  const float* __restrict__ cb = codebooks + (static_cast<int64_t>(m0) * 256 + j) * DSUB;
+// One table entry computed directly from the codebook, with the operation order
+// of the reference's table build: sum_u (r[m*dsub+u] - B[m][code][u])^2 left to
+// right from +0 (binary16-rounded for F16 tables).
+template <int FD, bool F16>
+__device__ __forceinline__ float direct_entry(const float* resid, const float* __restrict__ codebooks,
+                                              int m, int code, int ks, int dsub) {
+  const int d = FD > 0 ? FD : dsub;
+  const float* __restrict__ cw = codebooks + (static_cast<int64_t>(m) * ks + code) * d;
+  const float* r = resid + m * d;
+  float acc = 0.f;
+  if constexpr (FD > 0) {
+    Codeword<FD> c;
+    c.load(cw);
 #pragma unroll
-  for (int g0 = 0; g0 < kBlock; g0 += kGroup) {
-    Codeword<DSUB> cw[kGroup];
-#pragma unroll
-    for (int i = 0; i < kGroup; ++i) {
-      if (g0 + i < mb) cw[i].load(cb + (g0 + i) * 256 * DSUB);
+    for (int u = 0; u < FD; ++u) {
+      const float t = r[u] - c.v[u];
+      acc = acc + t * t;
     }
-#pragma unroll
-    for (int i = 0; i < kGroup; ++i) {
-      if (g0 + i < mb) {
-        const float* r = resid + (m0 + g0 + i) * DSUB;
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < DSUB; ++u) {
-          const float t = r[u] - cw[i].v[u];
-          acc = acc + t * t;
-        }
-        if (F16) {
-          lut16[(g0 + i) * 256 + j] = __half_as_ushort(__float2half_rn(acc));
-        } else {
-          lut32[(g0 + i) * 256 + j] = acc;
-        }
-      }
+  } else {
+    for (int u = 0; u < d; ++u) {
+      const float t = r[u] - cw[u];
+      acc = acc + t * t;
     }
   }
+  if (F16) acc = __half2float(__float2half_rn(acc));
+  return acc;
 }
 
-// Builds the table slice of subspaces [m0, m0 + mb) into LDS: entry
-// (m - m0) * ks + j = sum_u (r[m*dsub+u] - B[m][j][u])^2, left to right from +0.
-template <int DSUB, bool F16>
-__device__ __forceinline__ void build_slice(const float* resid, const float* __restrict__ codebooks,
-                                            int m0, int mb, int ks, int ks_log2, int dsub,
-                                            float* lut32, uint16_t* lut16) {
-  if constexpr (DSUB == 1 || DSUB == 2 || DSUB == 4 || DSUB == 8) {
-    if (ks == 256) {
-      build_slice_256<DSUB, F16>(resid, codebooks, m0, mb, lut32, lut16);
-      return;
-    }
-  }
-  const int d = DSUB > 0 ? DSUB : dsub;
-  const int slice = mb << ks_log2;
-  for (int e = threadIdx.x; e < slice; e += 256) {
-    const int m = m0 + (e >> ks_log2);
-    const float* r = resid + m * d;
-    const float* __restrict__ cw = codebooks + (static_cast<int64_t>(m) * ks + (e & (ks - 1))) * d;
-    float acc = 0.f;
-    if (DSUB > 0) {
-#pragma unroll
-      for (int u = 0; u < DSUB; ++u) {
-        const float t = r[u] - cw[u];
-        acc = acc + t * t;
-      }
-    } else {
-      for (int u = 0; u < d; ++u) {
-        const float t = r[u] - cw[u];
-        acc = acc + t * t;
-      }
-    }
-    if (F16) {
-      lut16[e] = __half_as_ushort(__float2half_rn(acc));
-    } else {
-      lut32[e] = acc;
-    }
-  }
+// Squared distance from r to the range [lo, hi] packed as binary16 lo | hi << 16
+// (the nearest point of the range is med3(r, lo, hi); both halves widen exactly).
+__device__ __forceinline__ float box_e2(float r, uint32_t b) {
+  const float lo = __half2float(__ushort_as_half(static_cast<uint16_t>(b & 0xffffu)));
+  const float hi = __half2float(__ushort_as_half(static_cast<uint16_t>(b >> 16)));
+  const float e = r - __builtin_amdgcn_fmed3f(r, lo, hi);
+  return e * e;
 }
 
-// Byte offset of (packed row pos, block b) in the tiled code layout.
-__device__ __forceinline__ int64_t code_offset(int64_t pos, int b, int nblocks) {
-  return (pos / kTile) * (static_cast<int64_t>(nblocks) * kTile * kBlock) +
-         static_cast<int64_t>(b) * (kTile * kBlock) + (pos % kTile) * kBlock;
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// One block's table slice lives in static LDS (its address is then a link-time
-// constant, folded into the table reads' immediate offsets); the rest is dynamic.
-constexpr size_t kLutBytes = static_cast<size_t>(kBlock) * 256 * 4;
+constexpr int kQueueCap = 128;
+// At most this many segments share one bound pass (at least 4 lanes each).
+constexpr int kSegPerPass = 16;
+// Rounding allowances of the lower bounds (valid for up to OVVS_MAX_BOX_DIMS box
+// dimensions and as many subspaces): a threshold raised by 2^-10 relative and a
+// tail bound lowered by 2^-10 relative cover every rounding of the bound sums and
+// of the scores they bound.
+constexpr float kBoundUp = 1.0f + 0x1p-10f;
+constexpr float kBoundDown = 1.0f - 0x1p-10f;
 
 struct ScanLayout {
-  size_t merge_bytes;  // the final cross-wave merge of the wave lists
-  size_t resid_off;
-  size_t thr_off;
-  size_t any_off;
-  size_t bufk_off;
-  size_t bufp_off;
+  size_t bufk_off;   // per wave: candidate keys [kBufCap]
+  size_t bufp_off;   //           candidate positions [kBufCap]
+  size_t qpos_off;   //           survivor queue positions [kQueueCap]
+  size_t qsc_off;    //           survivor queue partial scores [kQueueCap]
+  size_t work_bytes; // the above, or the final cross-wave merge (aliased)
+  size_t query_off;  // the query row [dim_pad]
+  size_t resid_off;  // per wave: residual of its current list [dim_pad]
+  size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
+  size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
+  size_t table_off;  // [7][P] per probe rank: list, rows, ordinal base, first segment,
+                     //        segments, first scan position, list bound
   size_t total;
 };
 
-__host__ __device__ inline ScanLayout scan_layout(int dim, int kpl) {
+__host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   ScanLayout L;
-  L.merge_bytes = round16(static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4));
-  L.resid_off = L.merge_bytes;
-  L.thr_off = L.resid_off + round16(static_cast<size_t>(dim) * 4);
-  L.any_off = L.thr_off + kWaves * 8;
-  L.bufk_off = L.any_off + round16(2 * kWaves * 4);
+  const size_t dim_pad = static_cast<size_t>((dim + 3) & ~3);
+  L.bufk_off = 0;
   L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
-  L.total = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
+  L.qpos_off = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
+  L.qsc_off = L.qpos_off + static_cast<size_t>(kWaves) * kQueueCap * 4;
+  const size_t cand = L.qsc_off + static_cast<size_t>(kWaves) * kQueueCap * 4;
+  const size_t merge = static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4);
+  L.work_bytes = round16(cand > merge ? cand : merge);
+  L.query_off = L.work_bytes;
+  L.resid_off = L.query_off + dim_pad * 4;
+  L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
+  L.misc_off = L.thr_off + (kWaves + 1) * 8;
+  L.table_off = L.misc_off + 16;
+  L.total = L.table_off + 7 * static_cast<size_t>(P) * 4;
   return L;
 }
 
-// FD > 0: the shape-specialised body for ks = 256, pq_m % 8 == 0 and dsub = FD
-// (every block full, table rows 1 KiB apart); FD = 0: any shape.
+// FD > 0: the shape-specialised body for ks = 256, pq_m % 8 == 0 and dsub = FD;
+// FD = 0: any shape.
 template <int KPL, bool F16, int FD>
 __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char* smem) {
-  const ScanLayout L = scan_layout(a.dim, KPL);
-  __shared__ __attribute__((aligned(16))) float s_lut[kLutBytes / 4];
-  float* lut32 = s_lut;
-  uint16_t* lut16 = reinterpret_cast<uint16_t*>(s_lut);
-  float* resid = reinterpret_cast<float*>(smem + L.resid_off);
-  uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
-  // Per wave: 1 while any of its rows of the current chunk is alive, in two
-  // slots used by alternate reads (any_rd is the slot the next read uses; every
-  // wave performs the same sequence of reads). A wave that leaves the block loop
-  // can start the next chunk and write its flag before a slower wave has read
-  // the flags that ended the loop: the write goes to the other slot, and it can
-  // be two reads ahead only after a barrier that the slower wave must reach.
-  int32_t* wave_any = reinterpret_cast<int32_t*>(smem + L.any_off);
-  int any_rd = 0;
+  const ScanLayout L = scan_layout(a.dim, KPL, a.P);
+  const int dim_pad = (a.dim + 3) & ~3;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = lane_id(), tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  float* qs = reinterpret_cast<float*>(smem + L.query_off);
+  float* resid = reinterpret_cast<float*>(smem + L.resid_off) + wave * dim_pad;
+  uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
   uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
   int32_t* bufp = reinterpret_cast<int32_t*>(smem + L.bufp_off) + wave * kBufCap;
+  int32_t* qpos = reinterpret_cast<int32_t*>(smem + L.qpos_off) + wave * kQueueCap;
+  float* qsc = reinterpret_cast<float*>(smem + L.qsc_off) + wave * kQueueCap;
 
   const int64_t q = blockIdx.x;
-  const float* __restrict__ qv = a.queries + q * a.dim;
   const int ks = a.ks;
-  const int ks_log2 = __ffs(ks) - 1;
   const int K = a.K;
-  const int nblocks = (a.pq_m + kBlock - 1) / kBlock;
-  // Bytes of one 64-row code tile, and the distance between a lane's rows i, i+1.
+  const int pq_m = a.pq_m;
+  const int dsub = FD > 0 ? FD : a.dsub;
+  const int nblocks = (pq_m + kBlock - 1) / kBlock;
+  const int mb0 = pq_m < kBlock ? pq_m : kBlock;
+  const int box_dims = pq_m * dsub;
+  const uint32_t* __restrict__ boxes = a.seg_box;
+  const uint32_t* __restrict__ lboxes = a.list_box;
+  int32_t* misc = reinterpret_cast<int32_t*>(smem + L.misc_off);
+  int32_t* t_list = reinterpret_cast<int32_t*>(smem + L.table_off);
+  int32_t* t_rows = t_list + a.P;
+  uint32_t* t_ord = reinterpret_cast<uint32_t*>(t_rows + a.P);
+  int32_t* t_sg0 = reinterpret_cast<int32_t*>(t_ord + a.P);
+  int32_t* t_nseg = t_sg0 + a.P;
+  int32_t* t_first = t_nseg + a.P;
+  float* t_lbound = reinterpret_cast<float*>(t_first + a.P);
+  // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
-  const uint32_t row_step = (kThreads / kTile) * tile_bytes;
+
+  for (int t = static_cast<int>(threadIdx.x); t < a.dim; t += kThreads) qs[t] = a.queries[q * a.dim + t];
+  if (lane == 0) wave_thr[wave] = kNoKey;
+  if (threadIdx.x == 0) wave_thr[kWaves] = kNoKey;
+  // Probe table: list, rows, segment range and first scan position per rank (an
+  // invalid probe id is marked -1 with no rows: the search then fails).
+  for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
+    const int l = a.probes[q * a.P + t];
+    const bool ok = static_cast<uint32_t>(l) < static_cast<uint32_t>(a.nlist);
+    const int lv = ok ? l : 0;
+    const int32_t sg0 = a.list_seg[lv];
+    const int32_t nseg = a.list_seg[lv + 1] - sg0;
+    t_list[t] = ok ? l : -1;
+    t_rows[t] = ok ? static_cast<int32_t>(a.list_offsets[lv + 1] - a.list_offsets[lv]) : 0;
+    t_sg0[t] = sg0;
+    t_nseg[t] = ok ? nseg : 0;
+    t_first[t] = (ok && nseg > 0) ? a.seg_start[sg0] : 0;
+  }
+  __syncthreads();
+  // Lower bound of every probed list's scores from its box (all four waves, the
+  // loads of many lists in flight together): the sum over the subspace dimensions
+  // of the squared distance from the residual q - c to the box. A list whose
+  // bound exceeds the K-th best score when its turn comes is skipped without
+  // touching memory.
+  if (lboxes) {
+    constexpr int kLanes = 4;  // per list
+    const int g = lane & (kLanes - 1);
+    const int chunk = (box_dims + kLanes - 1) / kLanes;
+    for (int base = 0; base < a.P; base += kThreads / kLanes) {
+      const int p = base + static_cast<int>(threadIdx.x) / kLanes;
+      float e = 0.f;
+      if (p < a.P && t_rows[p] > 0) {
+        const int l = t_list[p];
+        const uint32_t* __restrict__ lb = lboxes + static_cast<size_t>(l) * static_cast<size_t>(box_dims);
+        const float* __restrict__ cl = a.centroids + static_cast<int64_t>(l) * a.dim;
+        const int d1 = (g + 1) * chunk < box_dims ? (g + 1) * chunk : box_dims;
+        for (int db = g * chunk; db < d1; db += 8) {
+          // Indices past the chunk are clamped to its last dimension (the loads stay
+          // unconditional) and their terms replaced by +0.
+          float cv8[8];
+          uint32_t bx8[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int d = db + i < d1 ? db + i : d1 - 1;
+            cv8[i] = cl[d];
+            bx8[i] = lb[d];
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int d = db + i < d1 ? db + i : d1 - 1;
+            const float t = box_e2(qs[d] - cv8[i], bx8[i]);
+            e = e + (db + i < d1 ? t : 0.f);
+          }
+        }
+      }
+      e = e + __shfl_xor(e, 1, 64);
+      e = e + __shfl_xor(e, 2, 64);
+      if (p < a.P && g == 0) t_lbound[p] = e;
+    }
+  }
+  // Ordinal bases (exclusive prefix sums of the rows) and the end of phase 0:
+  // the first ranks holding 2K rows.
+  if (wave == 0) {
+    uint32_t base = 0;
+    int bad = 0, p0 = -1;
+    for (int c = 0; c < a.P; c += 64) {
+      const int t = c + lane;
+      const uint32_t r = t < a.P ? static_cast<uint32_t>(t_rows[t]) : 0u;
+      bad |= (t < a.P && t_list[t] < 0) ? 1 : 0;
+      uint32_t incl = r;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+      }
+      if (t < a.P) t_ord[t] = base + incl - r;
+      const uint64_t reach = __ballot(t < a.P && static_cast<uint64_t>(base) + incl >= 2u * static_cast<uint64_t>(K));
+      if (p0 < 0 && reach) p0 = c + __builtin_ctzll(reach) + 1;
+      base += __shfl(incl, 63, 64);
+    }
+    const uint64_t anybad = __ballot(bad != 0);
+    if (lane == 0) {
+      misc[0] = p0 < 0 ? a.P : p0;
+      misc[1] = anybad ? 1 : 0;
+    }
+  }
+  __syncthreads();
 
   uint64_t lk[KPL];
   int32_t lp[KPL];
@@ -348,15 +421,27 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     lk[j] = kNoKey;
     lp[j] = -1;
   }
-  uint64_t thr = kNoKey;
-  int cnt = 0;
+  uint64_t thr = kNoKey;  // the wave's own K-th key
+  // Score of the smallest K-th key any wave has published, and that score
+  // raised by the bound allowance.
+  float thr_f = __builtin_inff(), thr_hi = __builtin_inff();
+  int cnt = 0, qcnt = 0;
   uint32_t ord_base = 0;
   unsigned long long rows_total = 0, tasks = 0;
-  int bad_probe = 0;
-  if (lane == 0) wave_thr[wave] = kNoKey;
 
-  // Merges the first min(cnt, 64) buffered candidates into the wave's list and
-  // republishes the wave's threshold.
+  auto refresh = [&]() {
+    uint64_t t = wave_thr[0];
+#pragma unroll
+    for (int w = 1; w <= kWaves; ++w) t = wave_thr[w] < t ? wave_thr[w] : t;
+    thr_f = key_score(t);
+    thr_hi = thr_f * kBoundUp;
+  };
+  auto publish = [&]() {
+    thr = kth_key<KPL>(lk, K);
+    if (lane == 0) wave_thr[wave] = thr;
+    refresh();
+  };
+  // Merges the first min(cnt, 64) buffered candidates into the wave's list.
   auto flush = [&]() {
     const int take = cnt < 64 ? cnt : 64;
     uint64_t bk = lane < take ? bufk[lane] : kNoKey;
@@ -371,194 +456,281 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     cnt = rest;
     sort64(bk, bp);
     merge64<KPL>(lk, lp, bk, bp);
-    thr = kth_key<KPL>(lk, K);
-    if (lane == 0) wave_thr[wave] = thr;
+    publish();
+  };
+  // Rows with their complete score (lanes with ok) are offered to the wave's list.
+  auto offer = [&](bool ok, float score, int32_t pos) {
+    uint64_t key = kNoKey;
+    if (ok) key = make_key(score, ord_base + static_cast<uint32_t>(a.rord[pos]));
+    const bool pass = key < thr;
+    const uint64_t bal = __ballot(pass);
+    if (bal) {
+      const int before = __popcll(bal & ((1ull << lane) - 1ull));
+      if (pass) {
+        bufk[cnt + before] = key;
+        bufp[cnt + before] = pos;
+      }
+      cnt += __popcll(bal);
+      if (cnt >= 64) flush();
+    }
+  };
+  // Completes up to 64 queued rows (scored through block 0) with the entries of
+  // their remaining blocks, in subspace order; a row whose partial sum exceeds
+  // the K-th best score already is dropped (entries are >= +0, so partial sums
+  // never decrease).
+  auto finish_queue = [&]() {
+    const int take = qcnt < 64 ? qcnt : 64;
+    const int32_t pos = lane < take ? qpos[lane] : 0;
+    float sc = lane < take ? qsc[lane] : 0.f;
+    const int rest = qcnt - take;
+    if (lane < rest) {
+      const int32_t p2 = qpos[64 + lane];
+      const float s2 = qsc[64 + lane];
+      qpos[lane] = p2;
+      qsc[lane] = s2;
+    }
+    qcnt = rest;
+    bool alive = lane < take;
+    auto code_word = [&](int b) {
+      return *reinterpret_cast<const uint2*>(a.codes + static_cast<size_t>(pos >> 6) * tile_bytes +
+                                             b * (kTile * kBlock) + (pos & (kTile - 1)) * kBlock);
+    };
+    uint2 wnext = make_uint2(0u, 0u);
+    if (alive && nblocks > 1) wnext = code_word(1);
+    for (int b = 1; b < nblocks; ++b) {
+      if (__ballot(alive) == 0) break;
+      const int m0 = b * kBlock;
+      const int mb = pq_m - m0 < kBlock ? pq_m - m0 : kBlock;
+      const uint2 w = wnext;
+      // The next block's code word is requested before this block's entries.
+      if (alive && b + 1 < nblocks) wnext = code_word(b + 1);
+      if (alive) {
+        const uint32_t wv[2] = {w.x, w.y};
+        if (FD > 0) {
+          float v[kBlock];
+#pragma unroll
+          for (int j = 0; j < kBlock; ++j) {
+            const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+            v[j] = direct_entry<FD, F16>(resid, a.codebooks, m0 + j, code, ks, dsub);
+          }
+#pragma unroll
+          for (int j = 0; j < kBlock; ++j) sc = sc + v[j];
+        } else {
+          for (int j = 0; j < mb; ++j) {
+            const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+            sc = sc + direct_entry<FD, F16>(resid, a.codebooks, m0 + j, code, ks, dsub);
+          }
+        }
+      }
+      alive = alive && !(sc > thr_f);
+    }
+    offer(alive, sc, pos);
   };
 
-  for (int p = 0; p < a.P; ++p) {
-    int l = a.probes[q * a.P + p];
-    if (static_cast<uint32_t>(l) >= static_cast<uint32_t>(a.nlist)) {
-      bad_probe = 1;  // reported at the end (the search then fails), never dereferenced
-      l = 0;
+  // Phase 0: the nearest lists, until they hold 2K rows (or all of them), are
+  // scanned by all four waves together (each takes the 64-row tiles of index
+  // w mod 4), so that every wave starts the rest with a threshold: at the end of
+  // the phase the K-th best key over all four lists is published to every wave.
+  // Then wave w takes the remaining lists of rank p0 + w, p0 + w + 4, ...
+  const int p0 = misc[0];
+  for (int it = 0;; ++it) {
+    int p;
+    if (it < p0) {
+      p = it;
+    } else {
+      if (it == p0) {
+        // Every wave has folded its phase-0 candidates; wave 0 merges copies of
+        // the four lists and publishes the K-th key of the union.
+        constexpr int M = 64 * KPL;
+        __syncthreads();
+        uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) mk[wave * M + j * 64 + lane] = lk[j];
+        __syncthreads();
+        if (wave == 0) {
+          uint64_t tk[KPL];
+          int32_t tp[KPL];
+#pragma unroll
+          for (int j = 0; j < KPL; ++j) {
+            tk[j] = lk[j];
+            tp[j] = 0;
+          }
+          for (int w = 1; w < kWaves; ++w) {
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) {
+              const uint64_t rk = mk[w * M + (KPL - 1 - j) * 64 + (63 - lane)];
+              if (rk < tk[j]) tk[j] = rk;
+            }
+            bitonic_merge_asc<KPL>(tk, tp);
+          }
+          const uint64_t u = kth_key<KPL>(tk, K);
+          if (lane == 0) wave_thr[kWaves] = u;
+        }
+        __syncthreads();
+        refresh();
+      }
+      p = p0 + wave + kWaves * (it - p0);
+      if (p >= a.P) break;
     }
-    const int64_t begin = a.list_offsets[l];
-    const int64_t rows = a.list_offsets[l + 1] - begin;
+    const bool coop = it < p0;
+    const int32_t rows = t_rows[p];
     if (rows <= 0) continue;
-    ++tasks;
-    rows_total += static_cast<unsigned long long>(rows);
+    const int l = t_list[p];
+    ord_base = t_ord[p];
+    if (!coop || wave == 0) {
+      ++tasks;
+      rows_total += static_cast<unsigned long long>(rows);
+    }
 
-    __syncthreads();  // the previous list no longer reads resid
-    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
-    for (int t = threadIdx.x; t < a.dim; t += kThreads) resid[t] = qv[t] - cv[t];
+    const int sg0 = t_sg0[p];
+    const int nseg = t_nseg[p];
+    const int32_t first_pos = t_first[p];
 
-    for (int64_t c0 = 0; c0 < rows; c0 += kChunkRows) {
-      const int chunk = static_cast<int>(rows - c0 < kChunkRows ? rows - c0 : kChunkRows);
-      // Chunk rows are packed positions cpos + r, r = tid + i * kThreads. Their
-      // codes are addressed from a uniform base (the chunk's first tile) plus a
-      // 32-bit per-lane offset; rows i and i+1 of a lane are 4 tiles apart.
-      const int64_t cpos = begin + c0;
-      const uint8_t* __restrict__ cbase = a.codes + (cpos >> 6) * tile_bytes;
-      const uint32_t lrow = static_cast<uint32_t>(cpos & (kTile - 1)) + static_cast<uint32_t>(tid);
-      const uint32_t loff = (lrow >> 6) * tile_bytes + (lrow & (kTile - 1)) * kBlock;
-      float s[kRowsPerLane];
-      // live[i]: the wave's lanes whose row i is still a shortlist candidate
-      // (a wave-uniform lane mask, used directly as the execution mask).
-      uint64_t live[kRowsPerLane];
-#pragma unroll
-      for (int i = 0; i < kRowsPerLane; ++i) {
-        s[i] = 0.f;
-        const int r = tid + i * kThreads;
-        bool ok = r < chunk;
-        if (ok && a.bitset) {
-          const int64_t id = a.ids[cpos + r];
-          ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
-        }
-        live[i] = __builtin_amdgcn_ballot_w64(ok);
-      }
-      {
-        uint64_t any = 0;
-#pragma unroll
-        for (int i = 0; i < kRowsPerLane; ++i) any |= live[i];
-        if (lane == 0) wave_any[any_rd * kWaves + wave] = any != 0 ? 1 : 0;
-      }
-
-      for (int b = 0; b < nblocks; ++b) {
-        // Retires the previous block's table slice, publishes the waves' live
-        // flags (and resid, for the first block).
-        __syncthreads();
-        int any = wave_any[any_rd * kWaves];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) any |= wave_any[any_rd * kWaves + w];
-        any_rd ^= 1;
-        if (!any) break;
-        const int mb = FD > 0 ? kBlock : (a.pq_m - b * kBlock < kBlock ? a.pq_m - b * kBlock : kBlock);
+    // Whole-list bound first: the list's box contains every segment box.
+    refresh();
+    const bool skip = lboxes && t_lbound[p] > thr_hi;
+    if (!skip) {
+      const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
+      for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    for (int c0 = 0; c0 < (skip ? 0 : nseg); c0 += kSegPerPass) {
+      // S segments share this pass, G = 64 / S lanes each (S a power of two).
+      const int remaining = nseg - c0;
+      int gl = 2;  // log2(G)
+      while (gl < 6 && (32 >> gl) >= remaining) ++gl;
+      const int G = 1 << gl;
+      const int jl = lane >> gl;
+      const int g = lane & (G - 1);
+      const bool valid = jl < remaining && jl < kSegPerPass;
+      // Lower bound of every row's ADC score in the segment: per dimension the
+      // squared distance from the residual to the segment's (lo, hi) range; the
+      // entry of subspace m is a sum of its dimensions' squared differences, each
+      // at least that. e0: block 0's subspaces, et: the others. Lane g of a
+      // segment takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
+      float e0 = 0.f, et = 0.f;
+      if (valid && boxes) {
+        const uint32_t* __restrict__ box =
+            boxes + static_cast<size_t>(sg0 + c0 + jl) * static_cast<size_t>(box_dims);
+        const int c = (pq_m + G - 1) >> gl;
+        const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
         if constexpr (FD > 0) {
-          build_slice_256<FD, F16>(resid, a.codebooks, b * kBlock, kBlock, lut32, lut16);
+          // Sixteen dimensions of box requested at a time, then reduced.
+          constexpr int kBatch = FD >= 16 ? 1 : 16 / FD;
+          for (int mb = g * c; mb < m_end; mb += kBatch) {
+            // Subspaces past the chunk are clamped to its last one (the loads stay
+            // unconditional) and their terms replaced by +0.
+            uint32_t bx[kBatch][FD];
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+              const int m = mb + i < m_end ? mb + i : m_end - 1;
+#pragma unroll
+              for (int u = 0; u < FD; ++u) bx[i][u] = box[m * FD + u];
+            }
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+              const int m = mb + i < m_end ? mb + i : m_end - 1;
+              float part = 0.f;
+#pragma unroll
+              for (int u = 0; u < FD; ++u) part = part + box_e2(resid[m * FD + u], bx[i][u]);
+              part = mb + i < m_end ? part : 0.f;
+              e0 = e0 + (mb + i < kBlock ? part : 0.f);
+              et = et + (mb + i < kBlock ? 0.f : part);
+            }
+          }
         } else {
-        switch (a.dsub) {
-          case 1:
-            build_slice<1, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 1, lut32, lut16);
-            break;
-          case 2:
-            build_slice<2, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 2, lut32, lut16);
-            break;
-          case 4:
-            build_slice<4, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 4, lut32, lut16);
-            break;
-          case 8:
-            build_slice<8, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, 8, lut32, lut16);
-            break;
-          default:
-            build_slice<0, F16>(resid, a.codebooks, b * kBlock, mb, ks, ks_log2, a.dsub, lut32,
-                                lut16);
+          for (int m = g * c; m < m_end; ++m) {
+            float part = 0.f;
+            for (int u = 0; u < dsub; ++u) part = part + box_e2(resid[m * dsub + u], box[m * dsub + u]);
+            if (m < kBlock) {
+              e0 = e0 + part;
+            } else {
+              et = et + part;
+            }
+          }
         }
-        }
-        __syncthreads();
-        // Prune bound: the smallest K-th key any wave has published. Partial
-        // sums are >= +0 (or NaN, never pruned), so comparing floats against the
-        // decoded score is the same as comparing order-preserving keys.
-        uint64_t tmin = wave_thr[0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) tmin = wave_thr[w] < tmin ? wave_thr[w] : tmin;
-        const float thr_f = key_score(tmin);
-        const uint8_t* __restrict__ bbase = cbase + b * (kTile * kBlock);
-        // Recompute the per-row offsets in every block (one 32-bit add each)
-        // rather than let them be hoisted out of the block loop as 64-bit
-        // addresses held in registers across it.
-        uint32_t loff_b = loff;
-        asm volatile("" : "+v"(loff_b));
-        // Every live row's code word of this block is requested up front (codes
-        // that are not L2-resident cost an HBM round trip each).
-        constexpr int kD = kRowsPerLane;
-        uint2 wq[kD];
-#pragma unroll
-        for (int d = 0; d < kD; ++d) {
-          wq[d] = make_uint2(0u, 0u);
-          if (d < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[d]))
-            wq[d] = *reinterpret_cast<const uint2*>(bbase + (loff_b + d * row_step));
-        }
-#pragma unroll
-        for (int i = 0; i < kRowsPerLane; ++i) {
-          const uint2 w = wq[i % kD];
-          if (i + kD < kRowsPerLane && __builtin_amdgcn_inverse_ballot_w64(live[i + kD]))
-            wq[i % kD] = *reinterpret_cast<const uint2*>(bbase + (loff_b + (i + kD) * row_step));
-          // Uniform skip; within a live row every lane scores its code word (a
-          // dead lane's word is an earlier row's or zero, so its table reads stay
-          // in the slice) and only live lanes keep the result.
-          if (live[i] == 0) continue;
+      }
+      for (int o = 1; o < G; o <<= 1) {
+        e0 = e0 + __shfl_xor(e0, o, 64);
+        et = et + __shfl_xor(et, o, 64);
+      }
+      const float etot = e0 + et;
+      const float tl = et * kBoundDown;
+      refresh();
+      uint64_t kmask = __builtin_amdgcn_ballot_w64(valid && g == 0 && !(etot > thr_hi));
+      while (kmask) {
+        const int b = __builtin_ctzll(kmask);
+        kmask &= kmask - 1;
+        // The threshold may have dropped since the pass (other waves publish).
+        if (readlane_f(etot, b) > thr_hi) continue;
+        const float tl_j = readlane_f(tl, b);
+        const int gs = sg0 + c0 + (b >> gl);
+        const int32_t st = a.seg_start[gs];
+        const int32_t len = a.seg_len[gs];
+        for (int32_t t0 = 0; t0 < len; t0 += kTile) {
+          const int32_t pos0 = st + t0;
+          // Phase 0: tile i of the list belongs to wave i mod 4.
+          if (coop && (((pos0 - first_pos) >> 6) & (kWaves - 1)) != wave) continue;
+          const int32_t pos = pos0 + lane;
+          bool ok = lane < len - t0;
+          if (ok && a.bitset) {
+            const int64_t id = a.ids[pos];
+            ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
+          }
+          uint2 w = make_uint2(0u, 0u);
+          if (ok) {
+            w = *reinterpret_cast<const uint2*>(a.codes + static_cast<size_t>(pos0 >> 6) * tile_bytes +
+                                                lane * kBlock);
+          }
           const uint32_t wv[2] = {w.x, w.y};
-          float acc = s[i];
-          if (FD > 0 || (mb == kBlock && ks_log2 == 8)) {
-            // All eight table reads are independent: issue them before the
-            // left-to-right additions.
+          // Block 0: the first min(8, pq_m) entries, added left to right from +0.
+          float sc = 0.f;
+          if (FD > 0) {
             float v[kBlock];
 #pragma unroll
-            for (int j = 0; j < kBlock; ++j) {
-              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
-              v[j] = F16 ? __half2float(__ushort_as_half(lut16[j * 256 + code]))
-                         : lut32[j * 256 + code];
+            for (int jj = 0; jj < kBlock; ++jj) {
+              const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+              v[jj] = direct_entry<FD, F16>(resid, a.codebooks, jj, code, ks, dsub);
             }
 #pragma unroll
-            for (int j = 0; j < kBlock; ++j) acc = acc + v[j];
-          } else if constexpr (FD > 0) {
-          } else if (mb == kBlock) {
-#pragma unroll
-            for (int j = 0; j < kBlock; ++j) {
-              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
-              const int idx = (j << ks_log2) + code;
-              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
-            }
+            for (int jj = 0; jj < kBlock; ++jj) sc = sc + v[jj];
           } else {
-            for (int j = 0; j < mb; ++j) {
-              const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
-              const int idx = (j << ks_log2) + code;
-              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
+            for (int jj = 0; jj < mb0; ++jj) {
+              const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+              sc = sc + direct_entry<FD, F16>(resid, a.codebooks, jj, code, ks, dsub);
             }
           }
-          s[i] = acc;
-          live[i] &= __builtin_amdgcn_ballot_w64(!(acc > thr_f));
-        }
-        // For the next block's read.
-        uint64_t any_left = 0;
-#pragma unroll
-        for (int i = 0; i < kRowsPerLane; ++i) any_left |= live[i];
-        if (lane == 0) wave_any[any_rd * kWaves + wave] = any_left != 0 ? 1 : 0;
-      }
-
-      // Rows still alive carry their complete score: offer them to the wave's list.
-#pragma unroll
-      for (int i = 0; i < kRowsPerLane; ++i) {
-        if (i * kThreads >= chunk) break;
-        if (live[i] == 0) continue;
-        const int r = tid + i * kThreads;
-        const bool ok = __builtin_amdgcn_inverse_ballot_w64(live[i]);
-        const uint64_t key =
-            ok ? make_key(s[i], ord_base + static_cast<uint32_t>(c0) + static_cast<uint32_t>(r))
-               : kNoKey;
-        const bool pass = key < thr;
-        const uint64_t bal = __ballot(pass);
-        if (bal) {
-          const int before = __popcll(bal & ((1ull << lane) - 1ull));
-          if (pass) {
-            bufk[cnt + before] = key;
-            bufp[cnt + before] = static_cast<int32_t>(cpos) + r;
+          if (nblocks == 1) {
+            offer(ok, sc, pos);
+          } else {
+            // The rest of the row's score is at least the segment's tail bound.
+            const bool surv = ok && !((sc + tl_j) > thr_hi);
+            const uint64_t bal = __ballot(surv);
+            if (bal) {
+              const int before = __popcll(bal & ((1ull << lane) - 1ull));
+              if (surv) {
+                qpos[qcnt + before] = pos;
+                qsc[qcnt + before] = sc;
+              }
+              qcnt += __popcll(bal);
+              if (qcnt >= 64) finish_queue();
+            }
           }
-          cnt += __popcll(bal);
-          if (cnt >= 64) flush();
         }
-      }
-      // Fold what is left so the threshold used for pruning stays current: a few
-      // keys are inserted one by one, more go through the sort-and-merge.
-      if (cnt > 0 && cnt <= 8) {
-        for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
-        cnt = 0;
-        thr = kth_key<KPL>(lk, K);
-        if (lane == 0) wave_thr[wave] = thr;
-      } else if (cnt > 0) {
-        flush();
       }
     }
-    ord_base += static_cast<uint32_t>(rows);
+    while (qcnt > 0) finish_queue();
+    // Fold what is left so the published threshold stays current: a few keys are
+    // inserted one by one, more go through the sort-and-merge.
+    if (cnt > 0 && cnt <= 8) {
+      for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
+      cnt = 0;
+      publish();
+    } else {
+      while (cnt > 0) flush();
+    }
   }
 
   // Cross-wave merge: each wave publishes its sorted list, wave 0 folds in the rest.
@@ -570,6 +742,10 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   for (int j = 0; j < KPL; ++j) {
     mk[wave * M + j * 64 + lane] = lk[j];
     mp[wave * M + j * 64 + lane] = lp[j];
+  }
+  if (lane == 0) {
+    atomicAdd(&a.counters[0], rows_total);
+    atomicAdd(&a.counters[1], tasks);
   }
   __syncthreads();
   if (wave == 0) {
@@ -599,10 +775,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
     if (lane == 0) {
       a.out_count[q] = valid;
-      atomicAdd(&a.counters[0], rows_total);
-      atomicAdd(&a.counters[1], tasks);
       atomicAdd(&a.counters[2], static_cast<unsigned long long>(valid));
-      if (bad_probe) atomicAdd(&a.counters[3], 1ull);
+      if (misc[1]) atomicAdd(&a.counters[3], 1ull);
     }
   }
 }
@@ -639,7 +813,7 @@ hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   } else {
     fn = k_scan_long<KPL, F16>;
   }
-  if (lds + kLutBytes > 65536) {
+  if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds));
@@ -654,10 +828,12 @@ int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512
 }  // namespace
 
 extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
-                                          int32_t lut_f16, int32_t K) {
-  if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE) return 0;
+                                          int32_t lut_f16, int32_t K, int32_t P) {
+  if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE || P <= 0 ||
+      P > OVVS_HIP_MAX_PROBES)
+    return 0;
   (void)lut_f16;
-  const size_t b = scan_layout(dim, kpl_for(K)).total + kLutBytes;
+  const size_t b = scan_layout(dim, kpl_for(K), P).total;
   return b <= 160u * 1024u ? b : 0;
 }
 
@@ -666,15 +842,19 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   const OvvsScanArgs& a = *args;
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
-      !a.ids || !a.out_keys || !a.out_pos || !a.out_count || !a.counters || a.nq > 0x7fffffff ||
+      !a.ids || !a.rord || !a.list_seg || !a.seg_start || !a.seg_len || a.positions <= 0 ||
+      a.positions > 0x7fffffff || !a.out_keys || !a.out_pos || !a.out_count || !a.counters ||
+      a.nq > 0x7fffffff ||
       a.nlist <= 0 ||
       a.dim <= 0 || a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 ||
       (a.ks & (a.ks - 1)) != 0 || a.code_blocks != (a.pq_m + kBlock - 1) / kBlock ||
-      static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
+      static_cast<int64_t>(a.pq_m) * a.dsub > a.dim || a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE ||
+      (a.seg_box && static_cast<int64_t>(a.pq_m) * a.dsub > OVVS_MAX_BOX_DIMS))
     return hipErrorInvalidValue;
   const int kpl = kpl_for(a.K);
-  const size_t lds = scan_layout(a.dim, kpl).total;
-  if (lds + kLutBytes > 160u * 1024u) return hipErrorInvalidValue;
+  if (a.P > OVVS_HIP_MAX_PROBES) return hipErrorInvalidValue;
+  const size_t lds = scan_layout(a.dim, kpl, a.P).total;
+  if (lds > 160u * 1024u) return hipErrorInvalidValue;
   if (a.lut_f16) {
     switch (kpl) {
       case 1: return launch_scan<1, true>(a, lds, stream);
