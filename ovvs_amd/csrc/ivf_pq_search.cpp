@@ -143,6 +143,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     need += align256(static_cast<size_t>(nq) * R * 8);                    // shortlist keys
     need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
     need += align256(static_cast<size_t>(nq) * 4);                        // shortlist counts
+    need += align256(static_cast<size_t>(nq) * 16);                       // scan statistics
     need += align256(nqk * 8) + align256(nqk * 4);                        // staged outputs
     need += align256(4 * 8);                                              // counters
     need += (!device_io && bitset) ? align256(bitset_bytes) : 0;
@@ -160,6 +161,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     uint64_t* d_skeys = cv.take<uint64_t>(static_cast<size_t>(nq) * R);
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
     int32_t* d_scnt = cv.take<int32_t>(static_cast<size_t>(nq));
+    int32_t* d_sstats = cv.take<int32_t>(static_cast<size_t>(nq) * 4);
     int64_t* d_oid = cv.take<int64_t>(nqk);
     float* d_odist = cv.take<float>(nqk);
     unsigned long long* d_counters = cv.take<unsigned long long>(4);
@@ -255,8 +257,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.out_keys = d_skeys;
     sa.out_pos = d_spos;
     sa.out_count = d_scnt;
-    sa.counters = d_counters;
+    sa.out_stats = d_sstats;
     SEARCH_HIP(ovvs_hip_scan(&sa, s));
+    SEARCH_HIP(ovvs_hip_scan_stats(d_sstats, nq, d_counters, s));
     SEARCH_HIP(hipEventRecord(ev[3], s));
 
     OvvsRefineArgs ra{};
@@ -279,7 +282,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.invalid = d_counters + 3;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += 3 + 2 * chunks;
+    work.kernel_launches += 4 + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

@@ -138,13 +138,18 @@ struct OvvsScanArgs {
   uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
   int32_t* out_pos;            // [nq * K] scan positions
   int32_t* out_count;          // [nq]
-  unsigned long long* counters; // [4]: += scanned rows, += non-empty (query, list) tasks,
-                                //      += shortlist entries, += probe ids out of range
+  int32_t* out_stats;          // [nq * 4] per query: rows of the probed lists, non-empty
+                               // probed lists, shortlist entries, 1 if a probe id is out
+                               // of range
 };
 
-// Fused residual-LUT build (in LDS) + ADC code scan + per-query shortlist of
-// the K best (ADC score, dense ordinal) rows over all probed lists.
+// Code scan + per-query shortlist of the K best (ADC score, dense ordinal) rows
+// over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
+// counters[i] += sum over the queries of stats[q * 4 + i], i < 4 (the scan's
+// per-query statistics).
+hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq, unsigned long long* counters,
+                               hipStream_t stream);
 // Dynamic LDS bytes the scan kernel needs for these shapes, shortlist length and
 // probe count (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
 size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K,

@@ -351,50 +351,49 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // bound exceeds the K-th best score when its turn comes is skipped without
   // touching memory.
   if (lboxes) {
-    constexpr int kLanes = 4;  // per list
-    const int g = lane & (kLanes - 1);
-    const int chunk = (box_dims + kLanes - 1) / kLanes;
-    for (int base = 0; base < a.P; base += kThreads / kLanes) {
-      const int p = base + static_cast<int>(threadIdx.x) / kLanes;
-      float e = 0.f;
-      if (p < a.P && t_rows[p] > 0) {
-        const int l = t_list[p];
-        const uint32_t* __restrict__ lb = lboxes + static_cast<size_t>(l) * static_cast<size_t>(box_dims);
-        const float* __restrict__ cl = a.centroids + static_cast<int64_t>(l) * a.dim;
-        const int d1 = (g + 1) * chunk < box_dims ? (g + 1) * chunk : box_dims;
-        for (int db = g * chunk; db < d1; db += 8) {
-          // Indices past the chunk are clamped to its last dimension (the loads stay
-          // unconditional) and their terms replaced by +0.
-          float cv8[8];
-          uint32_t bx8[8];
+    // Wave w takes ranks w, w + 4, ...; lanes read consecutive dimensions of a
+    // list, four lists at a time.
+    constexpr int kLists = 4;
+    for (int p4 = wave * kLists; p4 < a.P; p4 += kWaves * kLists) {
+      float e[kLists];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int d = db + i < d1 ? db + i : d1 - 1;
-            cv8[i] = cl[d];
-            bx8[i] = lb[d];
-          }
+      for (int j = 0; j < kLists; ++j) e[j] = 0.f;
+      for (int d0 = 0; d0 < box_dims; d0 += 64) {
+        const int d = d0 + lane < box_dims ? d0 + lane : box_dims - 1;
+        float cv4[kLists];
+        uint32_t bx4[kLists];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int d = db + i < d1 ? db + i : d1 - 1;
-            const float t = box_e2(qs[d] - cv8[i], bx8[i]);
-            e = e + (db + i < d1 ? t : 0.f);
-          }
+        for (int j = 0; j < kLists; ++j) {
+          const int p = p4 + j < a.P ? p4 + j : a.P - 1;
+          const int l = t_rows[p] > 0 ? t_list[p] : 0;
+          cv4[j] = a.centroids[static_cast<int64_t>(l) * a.dim + d];
+          bx4[j] = lboxes[static_cast<size_t>(l) * static_cast<size_t>(box_dims) + d];
+        }
+        // Dimensions past box_dims read the last one and contribute +0.
+#pragma unroll
+        for (int j = 0; j < kLists; ++j) {
+          const float t = box_e2(qs[d] - cv4[j], bx4[j]);
+          e[j] = e[j] + (d0 + lane < box_dims ? t : 0.f);
         }
       }
-      e = e + __shfl_xor(e, 1, 64);
-      e = e + __shfl_xor(e, 2, 64);
-      if (p < a.P && g == 0) t_lbound[p] = e;
+#pragma unroll
+      for (int j = 0; j < kLists; ++j) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) e[j] = e[j] + __shfl_xor(e[j], o, 64);
+        if (lane == 0 && p4 + j < a.P) t_lbound[p4 + j] = e[j];
+      }
     }
   }
   // Ordinal bases (exclusive prefix sums of the rows) and the end of phase 0:
   // the first ranks holding 2K rows.
   if (wave == 0) {
     uint32_t base = 0;
-    int bad = 0, p0 = -1;
+    int bad = 0, p0 = -1, tasks_q = 0;
     for (int c = 0; c < a.P; c += 64) {
       const int t = c + lane;
       const uint32_t r = t < a.P ? static_cast<uint32_t>(t_rows[t]) : 0u;
       bad |= (t < a.P && t_list[t] < 0) ? 1 : 0;
+      tasks_q += __popcll(__ballot(t < a.P && r > 0));
       uint32_t incl = r;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -410,6 +409,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     if (lane == 0) {
       misc[0] = p0 < 0 ? a.P : p0;
       misc[1] = anybad ? 1 : 0;
+      misc[2] = static_cast<int32_t>(base);
+      misc[3] = tasks_q;
     }
   }
   __syncthreads();
@@ -427,7 +428,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   float thr_f = __builtin_inff(), thr_hi = __builtin_inff();
   int cnt = 0, qcnt = 0;
   uint32_t ord_base = 0;
-  unsigned long long rows_total = 0, tasks = 0;
 
   auto refresh = [&]() {
     uint64_t t = wave_thr[0];
@@ -577,10 +577,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     if (rows <= 0) continue;
     const int l = t_list[p];
     ord_base = t_ord[p];
-    if (!coop || wave == 0) {
-      ++tasks;
-      rows_total += static_cast<unsigned long long>(rows);
-    }
 
     const int sg0 = t_sg0[p];
     const int nseg = t_nseg[p];
@@ -743,10 +739,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     mk[wave * M + j * 64 + lane] = lk[j];
     mp[wave * M + j * 64 + lane] = lp[j];
   }
-  if (lane == 0) {
-    atomicAdd(&a.counters[0], rows_total);
-    atomicAdd(&a.counters[1], tasks);
-  }
   __syncthreads();
   if (wave == 0) {
     for (int w = 1; w < kWaves; ++w) {
@@ -775,8 +767,12 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
     if (lane == 0) {
       a.out_count[q] = valid;
-      atomicAdd(&a.counters[2], static_cast<unsigned long long>(valid));
-      if (misc[1]) atomicAdd(&a.counters[3], 1ull);
+      // Per-query statistics, summed by ovvs_hip_scan_stats (no atomics here:
+      // tens of thousands of workgroups adding into one address serialize).
+      a.out_stats[q * 4 + 0] = misc[2];
+      a.out_stats[q * 4 + 1] = misc[3];
+      a.out_stats[q * 4 + 2] = valid;
+      a.out_stats[q * 4 + 3] = misc[1];
     }
   }
 }
@@ -843,7 +839,7 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
       !a.ids || !a.rord || !a.list_seg || !a.seg_start || !a.seg_len || a.positions <= 0 ||
-      a.positions > 0x7fffffff || !a.out_keys || !a.out_pos || !a.out_count || !a.counters ||
+      a.positions > 0x7fffffff || !a.out_keys || !a.out_pos || !a.out_count || !a.out_stats ||
       a.nq > 0x7fffffff ||
       a.nlist <= 0 ||
       a.dim <= 0 || a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 ||
@@ -871,4 +867,41 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
     case 8: return launch_scan<8, false>(a, lds, stream);
     default: return launch_scan<16, false>(a, lds, stream);
   }
+}
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_scan_stats(const int32_t* __restrict__ stats, int64_t nq,
+                                                   unsigned long long* __restrict__ counters) {
+  unsigned long long acc[4] = {0, 0, 0, 0};
+  for (int64_t q = blockIdx.x * 256ll + threadIdx.x; q < nq; q += static_cast<int64_t>(gridDim.x) * 256) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += static_cast<uint32_t>(stats[q * 4 + i]);
+  }
+  __shared__ unsigned long long part[4][4];
+  const int lane = lane_id(), wave = static_cast<int>(threadIdx.x >> 6);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc[i] += shfl_xor_u64(acc[i], o);
+    if (lane == 0) part[wave][i] = acc[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    const unsigned long long v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] +
+                                 part[3][threadIdx.x];
+    if (v) atomicAdd(&counters[threadIdx.x], v);
+  }
+}
+
+}  // namespace
+
+extern "C" hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq,
+                                          unsigned long long* counters, hipStream_t stream) {
+  if (nq <= 0) return hipSuccess;
+  if (!stats || !counters) return hipErrorInvalidValue;
+  const int64_t blocks = (nq + 255) / 256;
+  hipLaunchKernelGGL(k_scan_stats, dim3(static_cast<uint32_t>(blocks < 64 ? blocks : 64)), dim3(256),
+                     0, stream, stats, nq, counters);
+  return hipGetLastError();
 }
