@@ -205,6 +205,64 @@ struct Codeword {
   }
 };
 
+// Table slice builders for the first phase (whole lists, all four waves): entry
+// (m - m0) * ks + j of the slice is sum_u (r[m*dsub+u] - B[m][j][u])^2, left to
+// right from +0 (binary16-rounded for F16 tables). For ks = 256 thread j computes
+// entry j of every subspace of the slice, its codebook loads (coalesced across
+// threads) issued a group of subspaces ahead of the arithmetic.
+template <int DSUB, bool F16>
+__device__ __forceinline__ void build_slice_256(const float* resid,
+                                                const float* __restrict__ codebooks, int m0,
+                                                float* lut32, uint16_t* lut16) {
+  constexpr int kGroup = DSUB <= 2 ? kBlock : 16 / DSUB;
+  const int j = static_cast<int>(threadIdx.x);
+  const float* __restrict__ cb = codebooks + (static_cast<int64_t>(m0) * 256 + j) * DSUB;
+#pragma unroll
+  for (int g0 = 0; g0 < kBlock; g0 += kGroup) {
+    Codeword<DSUB> cw[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) cw[i].load(cb + (g0 + i) * 256 * DSUB);
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const float* r = resid + (m0 + g0 + i) * DSUB;
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < DSUB; ++u) {
+        const float t = r[u] - cw[i].v[u];
+        acc = acc + t * t;
+      }
+      if (F16) {
+        lut16[(g0 + i) * 256 + j] = __half_as_ushort(__float2half_rn(acc));
+      } else {
+        lut32[(g0 + i) * 256 + j] = acc;
+      }
+    }
+  }
+}
+
+// Any shape: mb subspaces of ks entries, dsub dimensions each.
+template <bool F16>
+__device__ __forceinline__ void build_slice_any(const float* resid, const float* __restrict__ codebooks,
+                                                int m0, int mb, int ks, int ks_log2, int dsub,
+                                                float* lut32, uint16_t* lut16) {
+  const int slice = mb << ks_log2;
+  for (int e = static_cast<int>(threadIdx.x); e < slice; e += kThreads) {
+    const int m = m0 + (e >> ks_log2);
+    const float* r = resid + m * dsub;
+    const float* __restrict__ cw = codebooks + (static_cast<int64_t>(m) * ks + (e & (ks - 1))) * dsub;
+    float acc = 0.f;
+    for (int u = 0; u < dsub; ++u) {
+      const float t = r[u] - cw[u];
+      acc = acc + t * t;
+    }
+    if (F16) {
+      lut16[e] = __half_as_ushort(__float2half_rn(acc));
+    } else {
+      lut32[e] = acc;
+    }
+  }
+}
+
 // One table entry computed directly from the codebook, with the operation order
 // of the reference's table build: sum_u (r[m*dsub+u] - B[m][code][u])^2 left to
 // right from +0 (binary16-rounded for F16 tables).
@@ -266,8 +324,8 @@ struct ScanLayout {
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
   size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
-  size_t table_off;  // [7][P] per probe rank: list, rows, ordinal base, first segment,
-                     //        segments, first scan position, list bound
+  size_t table_off;  // [6][P] per probe rank: list, rows, ordinal base, first segment,
+                     //        segments, list bound
   size_t total;
 };
 
@@ -286,7 +344,7 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
   L.table_off = L.misc_off + 16;
-  L.total = L.table_off + 7 * static_cast<size_t>(P) * 4;
+  L.total = L.table_off + 6 * static_cast<size_t>(P) * 4;
   return L;
 }
 
@@ -322,15 +380,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   uint32_t* t_ord = reinterpret_cast<uint32_t*>(t_rows + a.P);
   int32_t* t_sg0 = reinterpret_cast<int32_t*>(t_ord + a.P);
   int32_t* t_nseg = t_sg0 + a.P;
-  int32_t* t_first = t_nseg + a.P;
-  float* t_lbound = reinterpret_cast<float*>(t_first + a.P);
+  float* t_lbound = reinterpret_cast<float*>(t_nseg + a.P);
   // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
 
   for (int t = static_cast<int>(threadIdx.x); t < a.dim; t += kThreads) qs[t] = a.queries[q * a.dim + t];
   if (lane == 0) wave_thr[wave] = kNoKey;
   if (threadIdx.x == 0) wave_thr[kWaves] = kNoKey;
-  // Probe table: list, rows, segment range and first scan position per rank (an
+  // Probe table: list, rows and segment range per rank (an
   // invalid probe id is marked -1 with no rows: the search then fails).
   for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
     const int l = a.probes[q * a.P + t];
@@ -342,7 +399,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     t_rows[t] = ok ? static_cast<int32_t>(a.list_offsets[lv + 1] - a.list_offsets[lv]) : 0;
     t_sg0[t] = sg0;
     t_nseg[t] = ok ? nseg : 0;
-    t_first[t] = (ok && nseg > 0) ? a.seg_start[sg0] : 0;
   }
   __syncthreads();
   // Lower bound of every probed list's scores from its box (all four waves, the
@@ -527,60 +583,155 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     offer(alive, sc, pos);
   };
 
-  // Phase 0: the nearest lists, until they hold 2K rows (or all of them), are
-  // scanned by all four waves together (each takes the 64-row tiles of index
-  // w mod 4), so that every wave starts the rest with a threshold: at the end of
-  // the phase the K-th best key over all four lists is published to every wave.
-  // Then wave w takes the remaining lists of rank p0 + w, p0 + w + 4, ...
-  const int p0 = misc[0];
-  for (int it = 0;; ++it) {
-    int p;
-    if (it < p0) {
-      p = it;
+  // Completes the queued rows and folds the buffered candidates into the wave's
+  // list, so that the published threshold is current: a few keys are inserted one
+  // by one, more go through the sort-and-merge.
+  auto settle = [&]() {
+    while (qcnt > 0) finish_queue();
+    if (cnt > 0 && cnt <= 8) {
+      for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
+      cnt = 0;
+      publish();
     } else {
-      if (it == p0) {
-        // Every wave has folded its phase-0 candidates; wave 0 merges copies of
-        // the four lists and publishes the K-th key of the union.
-        constexpr int M = 64 * KPL;
-        __syncthreads();
-        uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
-#pragma unroll
-        for (int j = 0; j < KPL; ++j) mk[wave * M + j * 64 + lane] = lk[j];
-        __syncthreads();
-        if (wave == 0) {
-          uint64_t tk[KPL];
-          int32_t tp[KPL];
-#pragma unroll
-          for (int j = 0; j < KPL; ++j) {
-            tk[j] = lk[j];
-            tp[j] = 0;
-          }
-          for (int w = 1; w < kWaves; ++w) {
-#pragma unroll
-            for (int j = 0; j < KPL; ++j) {
-              const uint64_t rk = mk[w * M + (KPL - 1 - j) * 64 + (63 - lane)];
-              if (rk < tk[j]) tk[j] = rk;
-            }
-            bitonic_merge_asc<KPL>(tk, tp);
-          }
-          const uint64_t u = kth_key<KPL>(tk, K);
-          if (lane == 0) wave_thr[kWaves] = u;
-        }
-        __syncthreads();
-        refresh();
-      }
-      p = p0 + wave + kWaves * (it - p0);
-      if (p >= a.P) break;
+      while (cnt > 0) flush();
     }
-    const bool coop = it < p0;
+  };
+
+  // Phase 0: the nearest lists, until they hold 2K rows (or all of them), are
+  // scored completely by all four waves together (64-row tiles in turn, table
+  // slices of 8 subspaces built in LDS from coalesced codebook reads), so that
+  // every wave starts the rest with a threshold; at the end of the phase the K-th
+  // best key of the union of the four lists is published to every wave. The
+  // slices live in the candidate-buffer and queue area, unused until a chunk's
+  // rows are offered.
+  constexpr int kP0Tiles = 4;  // tiles per wave per chunk
+  static_assert(static_cast<size_t>(kBlock) * 256 * 4 <=
+                    static_cast<size_t>(kWaves) * (kBufCap * 12 + kQueueCap * 8),
+                "table slice must fit the candidate buffers and survivor queues");
+  float* lut32 = reinterpret_cast<float*>(smem + L.bufk_off);
+  uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem + L.bufk_off);
+  const int ks_log2 = __ffs(ks) - 1;
+  const int p0 = misc[0];
+  for (int p = 0; p < p0; ++p) {
     const int32_t rows = t_rows[p];
     if (rows <= 0) continue;
     const int l = t_list[p];
     ord_base = t_ord[p];
+    const int sg0 = t_sg0[p];
+    const int sgl = sg0 + t_nseg[p] - 1;
+    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
+    for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // The list's segments are consecutive in scan order; padding rows have no
+    // in-list index.
+    const int32_t first = a.seg_start[sg0];
+    const int ntiles = (a.seg_start[sgl] + ((a.seg_len[sgl] + kTile - 1) & ~(kTile - 1)) - first) / kTile;
+    for (int c = 0; c < ntiles; c += kWaves * kP0Tiles) {
+      float sc[kP0Tiles];
+      bool ok[kP0Tiles];
+#pragma unroll
+      for (int i = 0; i < kP0Tiles; ++i) {
+        const int tile = c + wave + kWaves * i;
+        const int32_t pos = first + tile * kTile + lane;
+        sc[i] = 0.f;
+        ok[i] = tile < ntiles && a.rord[tile < ntiles ? pos : first] >= 0;
+        if (ok[i] && a.bitset) {
+          const int64_t id = a.ids[pos];
+          ok[i] = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
+        }
+      }
+      for (int b = 0; b < nblocks; ++b) {
+        const int m0 = b * kBlock;
+        const int mb = pq_m - m0 < kBlock ? pq_m - m0 : kBlock;
+        __syncthreads();  // every wave is done with the previous slice (or buffers)
+        if (FD > 0) {
+          build_slice_256<(FD > 0 ? FD : 1), F16>(resid, a.codebooks, m0, lut32, lut16);
+        } else {
+          build_slice_any<F16>(resid, a.codebooks, m0, mb, ks, ks_log2, dsub, lut32, lut16);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kP0Tiles; ++i) {
+          const int tile = c + wave + kWaves * i;
+          if (tile >= ntiles) continue;
+          uint2 w = make_uint2(0u, 0u);
+          if (ok[i]) {
+            w = *reinterpret_cast<const uint2*>(a.codes +
+                                                static_cast<size_t>((first >> 6) + tile) * tile_bytes +
+                                                b * (kTile * kBlock) + lane * kBlock);
+          }
+          const uint32_t wv[2] = {w.x, w.y};
+          float acc = sc[i];
+          if (FD > 0) {
+            float v[kBlock];
+#pragma unroll
+            for (int jj = 0; jj < kBlock; ++jj) {
+              const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+              v[jj] = F16 ? __half2float(__ushort_as_half(lut16[jj * 256 + code])) : lut32[jj * 256 + code];
+            }
+#pragma unroll
+            for (int jj = 0; jj < kBlock; ++jj) acc = acc + v[jj];
+          } else {
+            for (int jj = 0; jj < mb; ++jj) {
+              const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+              const int idx = (jj << ks_log2) + code;
+              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
+            }
+          }
+          sc[i] = acc;
+        }
+      }
+      __syncthreads();  // the slice area serves as candidate buffers again
+#pragma unroll
+      for (int i = 0; i < kP0Tiles; ++i) {
+        const int tile = c + wave + kWaves * i;
+        offer(ok[i], sc[i], first + tile * kTile + lane);
+      }
+      settle();
+    }
+  }
+  {
+    // Every wave has folded its phase-0 candidates; wave 0 merges copies of the
+    // four lists and publishes the K-th key of the union.
+    constexpr int M = 64 * KPL;
+    __syncthreads();
+    uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) mk[wave * M + j * 64 + lane] = lk[j];
+    __syncthreads();
+    if (wave == 0) {
+      uint64_t tk[KPL];
+      int32_t tp[KPL];
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        tk[j] = lk[j];
+        tp[j] = 0;
+      }
+      for (int w = 1; w < kWaves; ++w) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) {
+          const uint64_t rk = mk[w * M + (KPL - 1 - j) * 64 + (63 - lane)];
+          if (rk < tk[j]) tk[j] = rk;
+        }
+        bitonic_merge_asc<KPL>(tk, tp);
+      }
+      const uint64_t u = kth_key<KPL>(tk, K);
+      if (lane == 0) wave_thr[kWaves] = u;
+    }
+    __syncthreads();
+    refresh();
+  }
 
+  // The remaining lists: wave w takes ranks p0 + w, p0 + w + 4, ...
+  for (int p = p0 + wave; p < a.P; p += kWaves) {
+    const int32_t rows = t_rows[p];
+    if (rows <= 0) continue;
+    const int l = t_list[p];
+    ord_base = t_ord[p];
     const int sg0 = t_sg0[p];
     const int nseg = t_nseg[p];
-    const int32_t first_pos = t_first[p];
 
     // Whole-list bound first: the list's box contains every segment box.
     refresh();
@@ -655,11 +806,22 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const float etot = e0 + et;
       const float tl = et * kBoundDown;
       refresh();
-      uint64_t kmask = __builtin_amdgcn_ballot_w64(valid && g == 0 && !(etot > thr_hi));
-      while (kmask) {
-        const int b = __builtin_ctzll(kmask);
-        kmask &= kmask - 1;
-        // The threshold may have dropped since the pass (other waves publish).
+      // Kept segments, visited best bound first: rank = number of kept segments
+      // with a smaller (bound, index).
+      const bool lead = valid && g == 0 && !(etot > thr_hi);
+      const uint64_t kept = __builtin_amdgcn_ballot_w64(lead);
+      const uint32_t my_key = score_key(etot);
+      int rank = 0;
+      for (uint64_t m = kept; m;) {
+        const int b = __builtin_ctzll(m);
+        m &= m - 1;
+        const uint32_t kb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_key), b));
+        rank += (kb < my_key || (kb == my_key && b < lane)) ? 1 : 0;
+      }
+      const int nkept = __popcll(kept);
+      for (int r = 0; r < nkept; ++r) {
+        const int b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lead && rank == r));
+        // The threshold may have dropped since the pass.
         if (readlane_f(etot, b) > thr_hi) continue;
         const float tl_j = readlane_f(tl, b);
         const int gs = sg0 + c0 + (b >> gl);
@@ -667,8 +829,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         const int32_t len = a.seg_len[gs];
         for (int32_t t0 = 0; t0 < len; t0 += kTile) {
           const int32_t pos0 = st + t0;
-          // Phase 0: tile i of the list belongs to wave i mod 4.
-          if (coop && (((pos0 - first_pos) >> 6) & (kWaves - 1)) != wave) continue;
           const int32_t pos = pos0 + lane;
           bool ok = lane < len - t0;
           if (ok && a.bitset) {
@@ -717,16 +877,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
       }
     }
-    while (qcnt > 0) finish_queue();
-    // Fold what is left so the published threshold stays current: a few keys are
-    // inserted one by one, more go through the sort-and-merge.
-    if (cnt > 0 && cnt <= 8) {
-      for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
-      cnt = 0;
-      publish();
-    } else {
-      while (cnt > 0) flush();
-    }
+    settle();
   }
 
   // Cross-wave merge: each wave publishes its sorted list, wave 0 folds in the rest.
