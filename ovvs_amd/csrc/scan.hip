@@ -407,36 +407,45 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // bound exceeds the K-th best score when its turn comes is skipped without
   // touching memory.
   if (lboxes) {
-    // Wave w takes ranks w, w + 4, ...; lanes read consecutive dimensions of a
-    // list, four lists at a time.
-    constexpr int kLists = 4;
-    for (int p4 = wave * kLists; p4 < a.P; p4 += kWaves * kLists) {
+    // Wave w takes ranks 8w .. 8w + 7, 8w + 32 .. ; lanes read consecutive
+    // dimensions of a list; eight lists and two 64-dimension groups are requested
+    // before the arithmetic.
+    constexpr int kLists = 8;
+    for (int pb = wave * kLists; pb < a.P; pb += kWaves * kLists) {
       float e[kLists];
 #pragma unroll
       for (int j = 0; j < kLists; ++j) e[j] = 0.f;
-      for (int d0 = 0; d0 < box_dims; d0 += 64) {
-        const int d = d0 + lane < box_dims ? d0 + lane : box_dims - 1;
-        float cv4[kLists];
-        uint32_t bx4[kLists];
+      for (int d0 = 0; d0 < box_dims; d0 += 128) {
+        float cv[2][kLists];
+        uint32_t bx[2][kLists];
 #pragma unroll
-        for (int j = 0; j < kLists; ++j) {
-          const int p = p4 + j < a.P ? p4 + j : a.P - 1;
-          const int l = t_rows[p] > 0 ? t_list[p] : 0;
-          cv4[j] = a.centroids[static_cast<int64_t>(l) * a.dim + d];
-          bx4[j] = lboxes[static_cast<size_t>(l) * static_cast<size_t>(box_dims) + d];
+        for (int h = 0; h < 2; ++h) {
+          const int d = d0 + 64 * h + lane < box_dims ? d0 + 64 * h + lane : box_dims - 1;
+#pragma unroll
+          for (int j = 0; j < kLists; ++j) {
+            const int p = pb + j < a.P ? pb + j : a.P - 1;
+            const int l = t_rows[p] > 0 ? t_list[p] : 0;
+            cv[h][j] = a.centroids[static_cast<int64_t>(l) * a.dim + d];
+            bx[h][j] = lboxes[static_cast<size_t>(l) * static_cast<size_t>(box_dims) + d];
+          }
         }
         // Dimensions past box_dims read the last one and contribute +0.
 #pragma unroll
-        for (int j = 0; j < kLists; ++j) {
-          const float t = box_e2(qs[d] - cv4[j], bx4[j]);
-          e[j] = e[j] + (d0 + lane < box_dims ? t : 0.f);
+        for (int h = 0; h < 2; ++h) {
+          const int d = d0 + 64 * h + lane < box_dims ? d0 + 64 * h + lane : box_dims - 1;
+          const bool in = d0 + 64 * h + lane < box_dims;
+#pragma unroll
+          for (int j = 0; j < kLists; ++j) {
+            const float t = box_e2(qs[d] - cv[h][j], bx[h][j]);
+            e[j] = e[j] + (in ? t : 0.f);
+          }
         }
       }
 #pragma unroll
       for (int j = 0; j < kLists; ++j) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) e[j] = e[j] + __shfl_xor(e[j], o, 64);
-        if (lane == 0 && p4 + j < a.P) t_lbound[p4 + j] = e[j];
+        if (lane == 0 && pb + j < a.P) t_lbound[pb + j] = e[j];
       }
     }
   }
