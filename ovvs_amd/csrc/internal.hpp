@@ -55,9 +55,11 @@ struct ScanLayoutHost {
   std::vector<int32_t> list_seg;   // [nlist + 1] segment CSR
   std::vector<int32_t> seg_start;  // [nseg] first scan position
   std::vector<int32_t> seg_len;    // [nseg] rows
-  std::vector<uint32_t> seg_box;   // [nseg * box_dims] (lo, hi) of the reconstructions, as
+  std::vector<uint32_t> seg_box;   // [nseg * box_dims] (lo, hi) of the rows' reconstructions
+                                   // plus the list centroid (absolute coordinates), as
                                    // binary16 rounded outward, packed lo | hi << 16
   std::vector<uint32_t> list_box;  // [nlist * box_dims] the same over each whole list
+  float cmax = 0.f;                // max |centroid coordinate| (+inf if any is not finite)
   std::vector<int64_t> ids;        // [positions] row id, -1 for padding
   std::vector<int32_t> rord;       // [positions] index of the row within its list, -1 padding
   std::vector<uint8_t> codes;      // tiled codes by scan position (kernels.hpp)
@@ -70,6 +72,8 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
 // and the inverse of one half of it.
 uint32_t pack_box_fp16(float lo, float hi);
 float unpack_box_fp16(uint32_t b, int hi);
+// The range [c + lo, c + hi], rounded outward, packed the same way.
+uint32_t pack_abs_box_fp16(float c, float lo, float hi);
 
 // Device copy of an index. Codes, ids and in-list row indices are in scan order
 // (ScanLayoutHost); offsets are the reference's list CSR (rows per list and the
@@ -79,6 +83,7 @@ struct IndexDevice {
   int32_t code_blocks = 0;
   int64_t positions = 0;   // scan positions
   int32_t box_dims = 0;    // dimensions of each segment box (0: no boxes)
+  float box_cmax = 0.f;    // max |centroid coordinate| (ScanLayoutHost::cmax)
   DeviceBuffer centroids;  // [nlist * dim] f32
   DeviceBuffer cnorm;      // [nlist] f32
   DeviceBuffer cmfma;      // centroids as split-bf16 matrix-core operands (empty if dim > 128)

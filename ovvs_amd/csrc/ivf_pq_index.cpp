@@ -284,6 +284,7 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
   d->positions = lay.positions;
   // The scan's bound arithmetic covers boxes of up to OVVS_MAX_BOX_DIMS dimensions.
   d->box_dims = lay.box_dims <= OVVS_MAX_BOX_DIMS ? lay.box_dims : 0;
+  d->box_cmax = lay.cmax;
   const size_t nseg = lay.seg_start.size();
   hipStream_t s = res.stream;
   OVVS_TRY(alloc(d->centroids, centroids.size() * 4, work));

@@ -247,6 +247,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.seg_len = dv.seg_len.as<int32_t>();
     sa.seg_box = dv.box_dims > 0 ? dv.seg_box.as<uint32_t>() : nullptr;
     sa.list_box = dv.box_dims > 0 ? dv.list_box.as<uint32_t>() : nullptr;
+    sa.box_cmax = dv.box_cmax;
     sa.positions = dv.positions;
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();

@@ -125,9 +125,12 @@ struct OvvsScanArgs {
   const int32_t* list_seg;     // [nlist + 1] segment CSR
   const int32_t* seg_start;    // [nseg] first scan position of each segment (tile aligned)
   const int32_t* seg_len;      // [nseg] rows of each segment
-  const uint32_t* seg_box;     // [nseg * pq_m * dsub] (lo, hi) per dimension as binary16
-                               // rounded outward, packed lo | hi << 16; or nullptr
+  const uint32_t* seg_box;     // [nseg * pq_m * dsub] per dimension, the range of the rows'
+                               // reconstructions plus the list centroid (absolute
+                               // coordinates), binary16 rounded outward, packed
+                               // lo | hi << 16; or nullptr
   const uint32_t* list_box;    // [nlist * pq_m * dsub] the same over each list; or nullptr
+  float box_cmax;              // max |centroid coordinate| (+inf if any is not finite)
   int64_t positions;           // scan positions
   const uint8_t* codes;        // tiled codes by scan position, see OVVS_CODE_TILE_ROWS
   const int64_t* ids;          // [positions] row ids by scan position

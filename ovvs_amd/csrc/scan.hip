@@ -300,6 +300,17 @@ __device__ __forceinline__ float box_e2(float r, uint32_t b) {
   return e * e;
 }
 
+// Boxes are stored in absolute coordinates (the list centroid added), so the
+// distance is measured from q rather than from the residual fl(q - c) the table
+// entries use. Rounding moves each residual coordinate by at most s (2^-21 times
+// max|q| + max|c|), so over D dimensions the squared residual distance is at
+// least e - 2 s sqrt(D e) (Cauchy-Schwarz); the 2^-20 and the 2.02 also cover the
+// rounding of e itself. Returns that lower bound (NaN, which prunes nothing, when
+// e or s is not finite).
+__device__ __forceinline__ float box_bound(float e, float s, float D) {
+  return e * (1.f - 0x1p-20f) - 2.02f * s * __builtin_sqrtf(D * e);
+}
+
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
@@ -401,6 +412,20 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     t_nseg[t] = ok ? nseg : 0;
   }
   __syncthreads();
+  // Largest query coordinate magnitude, for the residual rounding allowance.
+  float qmax = 0.f;
+  for (int t = lane; t < a.dim; t += 64) {
+    const float v = __builtin_fabsf(qs[t]);
+    qmax = (v <= qmax) ? qmax : v;  // NaN propagates
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float v = __shfl_xor(qmax, o, 64);
+    qmax = (v <= qmax) ? qmax : v;
+  }
+  const float slack = 0x1p-21f * (qmax + a.box_cmax);
+  const float dims_all = static_cast<float>(box_dims);
+  const float dims_tail = static_cast<float>(box_dims - mb0 * dsub);
   // Lower bound of every probed list's scores from its box (all four waves, the
   // loads of many lists in flight together): the sum over the subspace dimensions
   // of the squared distance from the residual q - c to the box. A list whose
@@ -408,15 +433,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // touching memory.
   if (lboxes) {
     // Wave w takes ranks 8w .. 8w + 7, 8w + 32 .. ; lanes read consecutive
-    // dimensions of a list; eight lists and two 64-dimension groups are requested
-    // before the arithmetic.
+    // dimensions of a list's box; eight lists and two 64-dimension groups are
+    // requested before the arithmetic.
     constexpr int kLists = 8;
     for (int pb = wave * kLists; pb < a.P; pb += kWaves * kLists) {
       float e[kLists];
 #pragma unroll
       for (int j = 0; j < kLists; ++j) e[j] = 0.f;
       for (int d0 = 0; d0 < box_dims; d0 += 128) {
-        float cv[2][kLists];
         uint32_t bx[2][kLists];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -425,7 +449,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           for (int j = 0; j < kLists; ++j) {
             const int p = pb + j < a.P ? pb + j : a.P - 1;
             const int l = t_rows[p] > 0 ? t_list[p] : 0;
-            cv[h][j] = a.centroids[static_cast<int64_t>(l) * a.dim + d];
             bx[h][j] = lboxes[static_cast<size_t>(l) * static_cast<size_t>(box_dims) + d];
           }
         }
@@ -436,7 +459,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
           const bool in = d0 + 64 * h + lane < box_dims;
 #pragma unroll
           for (int j = 0; j < kLists; ++j) {
-            const float t = box_e2(qs[d] - cv[h][j], bx[h][j]);
+            const float t = box_e2(qs[d], bx[h][j]);
             e[j] = e[j] + (in ? t : 0.f);
           }
         }
@@ -445,7 +468,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       for (int j = 0; j < kLists; ++j) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) e[j] = e[j] + __shfl_xor(e[j], o, 64);
-        if (lane == 0 && pb + j < a.P) t_lbound[pb + j] = e[j];
+        if (lane == 0 && pb + j < a.P) t_lbound[pb + j] = box_bound(e[j], slack, dims_all);
       }
     }
   }
@@ -745,13 +768,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     // Whole-list bound first: the list's box contains every segment box.
     refresh();
     const bool skip = lboxes && t_lbound[p] > thr_hi;
-    if (!skip) {
-      const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
-      for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    // The residual (for table entries) is formed once a segment needs scoring.
+    bool have_resid = false;
     for (int c0 = 0; c0 < (skip ? 0 : nseg); c0 += kSegPerPass) {
       // S segments share this pass, G = 64 / S lanes each (S a power of two).
       const int remaining = nseg - c0;
@@ -762,10 +780,11 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const int g = lane & (G - 1);
       const bool valid = jl < remaining && jl < kSegPerPass;
       // Lower bound of every row's ADC score in the segment: per dimension the
-      // squared distance from the residual to the segment's (lo, hi) range; the
-      // entry of subspace m is a sum of its dimensions' squared differences, each
-      // at least that. e0: block 0's subspaces, et: the others. Lane g of a
-      // segment takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
+      // squared distance from the query to the segment's box; the entry of
+      // subspace m is a sum of its dimensions' squared residual differences, each
+      // at least that (up to box_bound's rounding allowance). e0: block 0's
+      // subspaces, et: the others. Lane g of a segment takes the subspaces
+      // [g * c, (g + 1) * c), c = ceil(pq_m / G).
       float e0 = 0.f, et = 0.f;
       if (valid && boxes) {
         const uint32_t* __restrict__ box =
@@ -790,7 +809,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
               const int m = mb + i < m_end ? mb + i : m_end - 1;
               float part = 0.f;
 #pragma unroll
-              for (int u = 0; u < FD; ++u) part = part + box_e2(resid[m * FD + u], bx[i][u]);
+              for (int u = 0; u < FD; ++u) part = part + box_e2(qs[m * FD + u], bx[i][u]);
               part = mb + i < m_end ? part : 0.f;
               e0 = e0 + (mb + i < kBlock ? part : 0.f);
               et = et + (mb + i < kBlock ? 0.f : part);
@@ -799,7 +818,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         } else {
           for (int m = g * c; m < m_end; ++m) {
             float part = 0.f;
-            for (int u = 0; u < dsub; ++u) part = part + box_e2(resid[m * dsub + u], box[m * dsub + u]);
+            for (int u = 0; u < dsub; ++u) part = part + box_e2(qs[m * dsub + u], box[m * dsub + u]);
             if (m < kBlock) {
               e0 = e0 + part;
             } else {
@@ -812,8 +831,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         e0 = e0 + __shfl_xor(e0, o, 64);
         et = et + __shfl_xor(et, o, 64);
       }
-      const float etot = e0 + et;
-      const float tl = et * kBoundDown;
+      const float etot = box_bound(e0 + et, slack, dims_all);
+      const float tb = box_bound(et, slack, dims_tail);
+      const float tl = (tb > 0.f ? tb : 0.f) * kBoundDown;
       refresh();
       // Kept segments, visited best bound first: rank = number of kept segments
       // with a smaller (bound, index).
@@ -828,6 +848,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         rank += (kb < my_key || (kb == my_key && b < lane)) ? 1 : 0;
       }
       const int nkept = __popcll(kept);
+      if (nkept > 0 && !have_resid) {
+        const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
+        for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        have_resid = true;
+      }
       for (int r = 0; r < nkept; ++r) {
         const int b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lead && rank == r));
         // The threshold may have dropped since the pass.

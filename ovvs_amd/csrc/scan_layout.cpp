@@ -92,6 +92,23 @@ uint32_t pack_box_fp16(float lo, float hi) {
 
 float unpack_box_fp16(uint32_t b, int hi) { return half_to_float(static_cast<uint16_t>(hi ? b >> 16 : b & 0xffffu)); }
 
+// The range [c + lo, c + hi] in absolute coordinates, rounded outward to binary16:
+// the sums are formed in double, widened by a relative 2^-40 (more than their
+// rounding error), rounded outward to float and then to binary16. A non-finite
+// centroid coordinate bounds nothing.
+uint32_t pack_abs_box_fp16(float c, float lo, float hi) {
+  constexpr float kInf = std::numeric_limits<float>::infinity();
+  if (!std::isfinite(c)) return pack_box_fp16(-kInf, kInf);
+  double a = static_cast<double>(c) + static_cast<double>(lo);
+  double b = static_cast<double>(c) + static_cast<double>(hi);
+  a -= std::fabs(a) * 0x1p-40;
+  b += std::fabs(b) * 0x1p-40;
+  float fa = static_cast<float>(a), fb = static_cast<float>(b);
+  if (static_cast<double>(fa) > a) fa = std::nextafter(fa, -kInf);
+  if (static_cast<double>(fb) < b) fb = std::nextafter(fb, kInf);
+  return pack_box_fp16(fa, fb);
+}
+
 }  // namespace ovvs
 
 namespace {
@@ -322,6 +339,7 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
       }
       // A dimension with a NaN entry (or no finite entry) bounds nothing.
       uint32_t* packed = out.seg_box.data() + static_cast<size_t>(sg) * D;
+      const float* cen = ix.centroids.data() + static_cast<size_t>(c) * static_cast<size_t>(ix.dim);
       for (int d = 0; d < D; ++d) {
         if (has_nan[static_cast<size_t>(d)] || !(box[2 * d] <= box[2 * d + 1])) {
           box[2 * d] = -std::numeric_limits<float>::infinity();
@@ -329,7 +347,7 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
         }
         lbox[2 * d] = std::min(lbox[2 * d], box[2 * d]);
         lbox[2 * d + 1] = std::max(lbox[2 * d + 1], box[2 * d + 1]);
-        packed[d] = ovvs::pack_box_fp16(box[2 * d], box[2 * d + 1]);
+        packed[d] = ovvs::pack_abs_box_fp16(cen[d], box[2 * d], box[2 * d + 1]);
       }
       p = (p + kT - 1) / kT * kT;
       ++sg;
@@ -337,11 +355,21 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
     // The list's box contains every segment box (an empty list keeps an empty
     // box; the scan never evaluates it).
     uint32_t* lpacked = out.list_box.data() + static_cast<size_t>(c) * D;
+    const float* cen = ix.centroids.data() + static_cast<size_t>(c) * static_cast<size_t>(ix.dim);
     for (int d = 0; d < D; ++d) {
-      lpacked[d] = lbox[2 * d] <= lbox[2 * d + 1] ? ovvs::pack_box_fp16(lbox[2 * d], lbox[2 * d + 1])
-                                                    : 0x7c00fc00u;
+      lpacked[d] = lbox[2 * d] <= lbox[2 * d + 1]
+                       ? ovvs::pack_abs_box_fp16(cen[d], lbox[2 * d], lbox[2 * d + 1])
+                       : 0x7c00fc00u;
     }
   });
+  // Largest centroid coordinate magnitude (+inf if any is not finite): bounds how
+  // far rounding can move a residual coordinate.
+  out.cmax = 0.f;
+  for (const float v : ix.centroids) {
+    const float m = std::fabs(v);
+    if (!(m <= out.cmax)) out.cmax = std::isfinite(m) ? m : std::numeric_limits<float>::infinity();
+    if (std::isinf(out.cmax)) break;
+  }
   return OVVS_STATUS_SUCCESS;
 }
 

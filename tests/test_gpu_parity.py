@@ -149,10 +149,10 @@ def test_random_indexes_against_oracle(ovvs, res, tmp_path):
 
 
 def test_multi_chunk_lists_against_oracle(ovvs, res, tmp_path):
-    """Lists of several thousand rows span several of the scan's 2048-row chunks,
-    and a tight shortlist (k = krefine = 10) prunes whole chunks after their first
-    block, so waves leave the block loop and start the next chunk at different
-    times. Results must match the oracle on every one of several repeats."""
+    """Lists of several thousand rows hold dozens of segments (several bound
+    passes of 16), phase 0 spans whole large lists, and a tight shortlist
+    (k = krefine = 10) prunes most segments. Results must match the oracle on
+    every one of several repeats."""
     rng = np.random.default_rng(23)
     dim, n, nlist = 32, 60000, 8
     centers = rng.standard_normal((16, dim)).astype(np.float32)
@@ -171,6 +171,63 @@ def test_multi_chunk_lists_against_oracle(ovvs, res, tmp_path):
         ids, d = ix.search(q, 10, 4, 10)
         assert_results_match(ids, d, oids, od, label=f"repeat {rep}")
         assert np.array_equal(_bits(d), _bits(od)), f"repeat {rep}"
+    ix.close()
+
+
+def test_ties_across_segments_keep_reference_order(ovvs, res, tmp_path):
+    """300 exact copies of one vector sit in one list, split over several segments
+    the scan visits in bound order; queries at and near the copy make the K-th
+    score a tie shared by every copy, so only the in-list ordinal decides which
+    copies are returned. Pruning compares strictly (a row is dropped only when its
+    bound exceeds the K-th score), so the result must be the reference's."""
+    rng = np.random.default_rng(31)
+    dim, n = 32, 4000
+    centers = rng.standard_normal((8, dim)).astype(np.float32)
+    data = (centers[rng.integers(0, 8, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    v = data[17].copy()
+    dup = rng.choice(n, 300, replace=False)
+    data[dup] = v
+    q = np.vstack([np.repeat(v[None], 8, 0),
+                   v[None] + 0.01 * rng.standard_normal((24, dim)).astype(np.float32)]).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=6, pq_m=8, pq_nbits=8, resources=res)
+    p = tmp_path / "ties.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for k, nprobe, krefine in [(10, 2, 10), (50, 3, 120), (1, 1, 1), (200, 6, 400)]:
+        ids, d = ix.search(q, k, nprobe, krefine)
+        oids, od = orc.search(q, k, nprobe, krefine)
+        assert np.array_equal(ids, oids), f"k{k} p{nprobe} r{krefine}"
+        assert np.array_equal(_bits(d), _bits(od)), f"k{k} p{nprobe} r{krefine}"
+    if REF_SO.exists():
+        ref = Reference()
+        rc, h = ref.load(p)
+        assert rc == 0
+        rc, rids, rd = ref.search(h, q, 10, 2, 10)
+        ids, d = ix.search(q, 10, 2, 10)
+        assert rc == 0 and np.array_equal(ids, rids) and np.array_equal(_bits(d), _bits(rd))
+        ref.destroy(h)
+        ref.close()
+    ix.close()
+
+
+def test_far_from_origin_data_against_oracle(ovvs, res, tmp_path):
+    """Vectors around +1000 in every coordinate: the segment boxes (absolute
+    coordinates, binary16 rounded outward) are coarse there and the residual
+    rounding allowance is at its largest; pruning must stay exact."""
+    rng = np.random.default_rng(37)
+    dim, n = 48, 8000
+    centers = (1000.0 + rng.standard_normal((24, dim))).astype(np.float32)
+    data = (centers[rng.integers(0, 24, n)] + 0.2 * rng.standard_normal((n, dim))).astype(np.float32)
+    q = (centers[rng.integers(0, 24, 300)] + 0.2 * rng.standard_normal((300, dim))).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=24, pq_m=24, pq_nbits=8, resources=res)
+    p = tmp_path / "far.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for k, nprobe, krefine in [(10, 6, 10), (10, 24, 64)]:
+        ids, d = ix.search(q, k, nprobe, krefine)
+        oids, od = orc.search(q, k, nprobe, krefine)
+        assert_results_match(ids, d, oids, od, label=f"k{k} p{nprobe}")
+        assert np.array_equal(_bits(d), _bits(od)), f"k{k} p{nprobe}"
     ix.close()
 
 
