@@ -965,12 +965,12 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   }
 }
 
-// The scan is latency-bound, so shortlists of up to 128 keys run at 8 waves per
-// SIMD (64 VGPRs): the row loop fits without spilling and only the rarely taken
-// shortlist merge keeps a few values in scratch. Longer register lists keep the
+// Shortlists of up to 128 keys run at 7 waves per SIMD (72 VGPRs): the scan is
+// latency-bound, and measured on C2 this balances occupancy against register
+// spills better than 8 (64 VGPRs) or 6 (80). Longer register lists keep the
 // compiler's own allocation.
 template <int KPL, bool F16, int FD>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_scan(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   scan_query<KPL, F16, FD>(a, smem);
