@@ -335,6 +335,8 @@ struct ScanLayout {
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
   size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
+  size_t slot_off;   // per wave: [2][kSegPerPass] int32, the segments of a bound pass and
+                     //           their list ranks
   size_t table_off;  // [6][P] per probe rank: list, rows, ordinal base, first segment,
                      //        segments, list bound
   size_t total;
@@ -354,7 +356,8 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.resid_off = L.query_off + dim_pad * 4;
   L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
-  L.table_off = L.misc_off + 16;
+  L.slot_off = L.misc_off + 16;
+  L.table_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * kSegPerPass * 4;
   L.total = L.table_off + 6 * static_cast<size_t>(P) * 4;
   return L;
 }
@@ -756,29 +759,53 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     refresh();
   }
 
-  // The remaining lists: wave w takes ranks p0 + w, p0 + w + 4, ...
-  for (int p = p0 + wave; p < a.P; p += kWaves) {
-    const int32_t rows = t_rows[p];
-    if (rows <= 0) continue;
-    const int l = t_list[p];
-    ord_base = t_ord[p];
-    const int sg0 = t_sg0[p];
-    const int nseg = t_nseg[p];
-
-    // Whole-list bound first: the list's box contains every segment box.
+  // The remaining lists, as a stream of segments per wave: wave w takes the lists
+  // of rank p0 + w, p0 + w + 4, ... whose list bound does not exceed the K-th best
+  // score, and evaluates their segments' bounds 16 at a time (a pass may span
+  // several lists, so that short lists do not leave lanes idle). Kept segments are
+  // then scored grouped by list, best bound first within a list.
+  int32_t* slot_seg = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * kSegPerPass;
+  int32_t* slot_p = slot_seg + kSegPerPass;
+  int sp = p0 + wave;  // next list rank of this wave
+  int s_off = 0;       // segments of list sp already taken
+  int cur_p = -1;      // list whose residual is in resid
+  for (;;) {
     refresh();
-    const bool skip = lboxes && t_lbound[p] > thr_hi;
-    // The residual (for table entries) is formed once a segment needs scoring.
-    bool have_resid = false;
-    for (int c0 = 0; c0 < (skip ? 0 : nseg); c0 += kSegPerPass) {
+    int filled = 0;
+    while (filled < kSegPerPass && sp < a.P) {
+      const int nseg = t_nseg[sp];
+      if (t_rows[sp] <= 0 || (lboxes && t_lbound[sp] > thr_hi)) {
+        sp += kWaves;
+        s_off = 0;
+        continue;
+      }
+      const int take = kSegPerPass - filled < nseg - s_off ? kSegPerPass - filled : nseg - s_off;
+      if (lane < take) {
+        slot_seg[filled + lane] = t_sg0[sp] + s_off + lane;
+        slot_p[filled + lane] = sp;
+      }
+      filled += take;
+      s_off += take;
+      if (s_off == nseg) {
+        sp += kWaves;
+        s_off = 0;
+      }
+    }
+    if (filled == 0) break;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
       // S segments share this pass, G = 64 / S lanes each (S a power of two).
-      const int remaining = nseg - c0;
+      const int remaining = filled;
       int gl = 2;  // log2(G)
       while (gl < 6 && (32 >> gl) >= remaining) ++gl;
       const int G = 1 << gl;
       const int jl = lane >> gl;
       const int g = lane & (G - 1);
-      const bool valid = jl < remaining && jl < kSegPerPass;
+      const bool valid = jl < remaining;
+      const int seg = valid ? slot_seg[jl] : 0;
+      const int pp = valid ? slot_p[jl] : 0;
       // Lower bound of every row's ADC score in the segment: per dimension the
       // squared distance from the query to the segment's box; the entry of
       // subspace m is a sum of its dimensions' squared residual differences, each
@@ -787,8 +814,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       // [g * c, (g + 1) * c), c = ceil(pq_m / G).
       float e0 = 0.f, et = 0.f;
       if (valid && boxes) {
-        const uint32_t* __restrict__ box =
-            boxes + static_cast<size_t>(sg0 + c0 + jl) * static_cast<size_t>(box_dims);
+        const uint32_t* __restrict__ box = boxes + static_cast<size_t>(seg) * static_cast<size_t>(box_dims);
         const int c = (pq_m + G - 1) >> gl;
         const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
         if constexpr (FD > 0) {
@@ -835,8 +861,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const float tb = box_bound(et, slack, dims_tail);
       const float tl = (tb > 0.f ? tb : 0.f) * kBoundDown;
       refresh();
-      // Kept segments, visited best bound first: rank = number of kept segments
-      // with a smaller (bound, index).
+      // Kept segments in (list, bound, slot) order: rank = number of kept segments
+      // before this one.
       const bool lead = valid && g == 0 && !(etot > thr_hi);
       const uint64_t kept = __builtin_amdgcn_ballot_w64(lead);
       const uint32_t my_key = score_key(etot);
@@ -844,24 +870,31 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       for (uint64_t m = kept; m;) {
         const int b = __builtin_ctzll(m);
         m &= m - 1;
+        const int pb = __builtin_amdgcn_readlane(pp, b);
         const uint32_t kb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_key), b));
-        rank += (kb < my_key || (kb == my_key && b < lane)) ? 1 : 0;
+        rank += (pb < pp || (pb == pp && (kb < my_key || (kb == my_key && b < lane)))) ? 1 : 0;
       }
       const int nkept = __popcll(kept);
-      if (nkept > 0 && !have_resid) {
-        const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
-        for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        have_resid = true;
-      }
       for (int r = 0; r < nkept; ++r) {
         const int b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lead && rank == r));
         // The threshold may have dropped since the pass.
         if (readlane_f(etot, b) > thr_hi) continue;
         const float tl_j = readlane_f(tl, b);
-        const int gs = sg0 + c0 + (b >> gl);
+        const int gs = __builtin_amdgcn_readlane(seg, b);
+        const int p = __builtin_amdgcn_readlane(pp, b);
+        if (p != cur_p) {
+          // A new list: complete the rows queued for the previous one (its residual
+          // and ordinal base), then form this list's residual.
+          settle();
+          const int l = t_list[p];
+          ord_base = t_ord[p];
+          const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
+          for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          cur_p = p;
+        }
         const int32_t st = a.seg_start[gs];
         const int32_t len = a.seg_len[gs];
         for (int32_t t0 = 0; t0 < len; t0 += kTile) {
@@ -914,8 +947,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
       }
     }
-    settle();
   }
+  settle();
 
   // Cross-wave merge: each wave publishes its sorted list, wave 0 folds in the rest.
   constexpr int M = 64 * KPL;
