@@ -10,7 +10,7 @@ n_probes=64, k=10, krefine=k, fp32 lookup tables, 10k-query batch.
 A step is one ovvsIvfPqSearchDevice call over the whole batch with queries and
 results already in HBM. value = queries / second over the timed steps.
 The JSON line also carries:
-  roofline      the fused LUT+scan+select kernel: algorithmic code bytes per
+  roofline      the code scan + select kernel: algorithmic code bytes per
                 launch (candidate_rows * pq_m from the library's telemetry)
                 divided by its average duration (HIP events on the library's
                 stream), against the 8 TB/s HBM peak;
@@ -381,7 +381,7 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "k_scan (fused LUT build + code scan + shortlist)",
+            "kernel": "k_scan (segment-bounded code scan + shortlist)",
             "algorithmic_bytes_per_launch": code_bytes,
             "avg_launch_ms": scan_s * 1e3,
         },
