@@ -53,6 +53,9 @@ struct ScanLayoutHost {
   int64_t positions = 0;           // scan positions: rows plus padding, a multiple of 64
   int32_t box_dims = 0;            // pq_m * dsub
   std::vector<int32_t> list_seg;   // [nlist + 1] segment CSR
+  std::vector<int32_t> list_grp;   // [nlist + 1] group CSR (groups of consecutive segments)
+  std::vector<int32_t> grp_seg;    // [ngrp + 1] first segment of each group
+  std::vector<uint32_t> grp_box;   // [ngrp * box_dims] union of the group's segment boxes
   std::vector<int32_t> seg_start;  // [nseg] first scan position
   std::vector<int32_t> seg_len;    // [nseg] rows
   std::vector<uint32_t> seg_box;   // [nseg * box_dims] (lo, hi) of the rows' reconstructions
@@ -98,6 +101,9 @@ struct IndexDevice {
   DeviceBuffer seg_len;    // [nseg] i32
   DeviceBuffer seg_box;    // [nseg * box_dims] packed binary16 (lo, hi)
   DeviceBuffer list_box;   // [nlist * box_dims] packed binary16 (lo, hi)
+  DeviceBuffer list_grp;   // [nlist + 1] i32
+  DeviceBuffer grp_seg;    // [ngrp + 1] i32
+  DeviceBuffer grp_box;    // [ngrp * box_dims] packed binary16 (lo, hi)
   DeviceBuffer dataset;    // [n * dim] f32
   DeviceBuffer xnorm;      // [n] f32
 };

@@ -301,7 +301,13 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
     OVVS_TRY(alloc(d->seg_box, std::max<size_t>(lay.seg_box.size(), 1) * 4, work));
     OVVS_TRY(alloc(d->list_box, lay.list_box.size() * 4, work));
     OVVS_TRY(h2d(d->list_box.get(), lay.list_box.data(), lay.list_box.size() * 4, s, work));
+    OVVS_TRY(alloc(d->grp_box, std::max<size_t>(lay.grp_box.size(), 1) * 4, work));
+    OVVS_TRY(h2d(d->grp_box.get(), lay.grp_box.data(), lay.grp_box.size() * 4, s, work));
   }
+  OVVS_TRY(alloc(d->list_grp, lay.list_grp.size() * 4, work));
+  OVVS_TRY(h2d(d->list_grp.get(), lay.list_grp.data(), lay.list_grp.size() * 4, s, work));
+  OVVS_TRY(alloc(d->grp_seg, lay.grp_seg.size() * 4, work));
+  OVVS_TRY(h2d(d->grp_seg.get(), lay.grp_seg.data(), lay.grp_seg.size() * 4, s, work));
   OVVS_TRY(alloc(d->dataset, dataset.size() * 4, work));
   OVVS_TRY(alloc(d->xnorm, static_cast<size_t>(n) * 4, work));
   OVVS_TRY(h2d(d->centroids.get(), centroids.data(), centroids.size() * 4, s, work));

@@ -248,6 +248,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.seg_box = dv.box_dims > 0 ? dv.seg_box.as<uint32_t>() : nullptr;
     sa.list_box = dv.box_dims > 0 ? dv.list_box.as<uint32_t>() : nullptr;
     sa.box_cmax = dv.box_cmax;
+    sa.list_grp = dv.list_grp.as<int32_t>();
+    sa.grp_seg = dv.grp_seg.as<int32_t>();
+    sa.grp_box = dv.box_dims > 0 ? dv.grp_box.as<uint32_t>() : nullptr;
     sa.positions = dv.positions;
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();

@@ -34,6 +34,9 @@ extern "C" {
 // reconstructions in every subspace dimension (its box). Rows keep their
 // index within the list, which is what orders candidates.
 #define OVVS_SEGMENT_ROWS 128
+// Segments are grouped (maximal subtrees of the segmentation with at most this many
+// segments), each group with the union of its segments' boxes.
+#define OVVS_GROUP_SEGMENTS 4
 // Boxes are used when pq_m * dsub is at most this (the scan's rounding-error
 // allowance for its lower bounds holds up to there).
 #define OVVS_MAX_BOX_DIMS 2048
@@ -130,6 +133,9 @@ struct OvvsScanArgs {
                                // coordinates), binary16 rounded outward, packed
                                // lo | hi << 16; or nullptr
   const uint32_t* list_box;    // [nlist * pq_m * dsub] the same over each list; or nullptr
+  const int32_t* list_grp;     // [nlist + 1] group CSR
+  const int32_t* grp_seg;      // [ngrp + 1] first segment of each group
+  const uint32_t* grp_box;     // [ngrp * pq_m * dsub] the same over each group; or nullptr
   float box_cmax;              // max |centroid coordinate| (+inf if any is not finite)
   int64_t positions;           // scan positions
   const uint8_t* codes;        // tiled codes by scan position, see OVVS_CODE_TILE_ROWS

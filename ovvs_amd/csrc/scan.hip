@@ -20,8 +20,11 @@
 //     (and the part after block 0). fp32 rounding is monotone, so the bounds hold
 //     for the rounded scores up to a small relative allowance.
 //   * A segment whose bound exceeds the K-th best score found so far cannot
-//     contribute: it is skipped without reading its codes. Segment bounds are
-//     evaluated 4-64 lanes per segment, up to 16 segments per pass.
+//     contribute: it is skipped without reading its codes. Consecutive segments
+//     (subtrees of the segmentation, at most four segments) form groups with the
+//     union of their boxes, and so does each list: a list or group whose bound
+//     exceeds the K-th best is skipped whole. Group and segment bounds are
+//     evaluated 4-64 lanes per box, up to 16 boxes per pass.
 //   * Rows of the other segments are read in 64-row code tiles (one coalesced
 //     512-byte access per wave and block) and scored through block 0 (the first 8
 //     subspaces). A row whose partial sum plus the segment's tail bound still
@@ -318,6 +321,8 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 constexpr int kQueueCap = 128;
 // At most this many segments share one bound pass (at least 4 lanes each).
 constexpr int kSegPerPass = 16;
+// Segment slots of one group pass (every group holds at most OVVS_GROUP_SEGMENTS).
+constexpr int kSegSlots = OVVS_GROUP_SEGMENTS * kSegPerPass;
 // Rounding allowances of the lower bounds (valid for up to OVVS_MAX_BOX_DIMS box
 // dimensions and as many subspaces): a threshold raised by 2^-10 relative and a
 // tail bound lowered by 2^-10 relative cover every rounding of the bound sums and
@@ -335,10 +340,10 @@ struct ScanLayout {
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
   size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
-  size_t slot_off;   // per wave: [2][kSegPerPass] int32, the segments of a bound pass and
-                     //           their list ranks
-  size_t table_off;  // [6][P] per probe rank: list, rows, ordinal base, first segment,
-                     //        segments, list bound
+  size_t slot_off;   // per wave: [2][kSegPerPass] int32, the groups of a bound pass and
+                     //           their list ranks; [2][kSegSlots], the same for segments
+  size_t table_off;  // [8][P] per probe rank: list, rows, ordinal base, first segment,
+                     //        segments, list bound, first group, groups
   size_t total;
 };
 
@@ -357,8 +362,8 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
   L.slot_off = L.misc_off + 16;
-  L.table_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * kSegPerPass * 4;
-  L.total = L.table_off + 6 * static_cast<size_t>(P) * 4;
+  L.table_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * (kSegPerPass + kSegSlots) * 4;
+  L.total = L.table_off + 8 * static_cast<size_t>(P) * 4;
   return L;
 }
 
@@ -395,13 +400,15 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* t_sg0 = reinterpret_cast<int32_t*>(t_ord + a.P);
   int32_t* t_nseg = t_sg0 + a.P;
   float* t_lbound = reinterpret_cast<float*>(t_nseg + a.P);
+  int32_t* t_g0 = reinterpret_cast<int32_t*>(t_lbound + a.P);
+  int32_t* t_ngrp = t_g0 + a.P;
   // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
 
   for (int t = static_cast<int>(threadIdx.x); t < a.dim; t += kThreads) qs[t] = a.queries[q * a.dim + t];
   if (lane == 0) wave_thr[wave] = kNoKey;
   if (threadIdx.x == 0) wave_thr[kWaves] = kNoKey;
-  // Probe table: list, rows and segment range per rank (an
+  // Probe table: list, rows, segment and group ranges per rank (an
   // invalid probe id is marked -1 with no rows: the search then fails).
   for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
     const int l = a.probes[q * a.P + t];
@@ -413,6 +420,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     t_rows[t] = ok ? static_cast<int32_t>(a.list_offsets[lv + 1] - a.list_offsets[lv]) : 0;
     t_sg0[t] = sg0;
     t_nseg[t] = ok ? nseg : 0;
+    const int32_t g0 = a.list_grp[lv];
+    t_g0[t] = g0;
+    t_ngrp[t] = ok ? a.list_grp[lv + 1] - g0 : 0;
   }
   __syncthreads();
   // Largest query coordinate magnitude, for the residual rounding allowance.
@@ -759,104 +769,147 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     refresh();
   }
 
-  // The remaining lists, as a stream of segments per wave: wave w takes the lists
-  // of rank p0 + w, p0 + w + 4, ... whose list bound does not exceed the K-th best
-  // score, and evaluates their segments' bounds 16 at a time (a pass may span
-  // several lists, so that short lists do not leave lanes idle). Kept segments are
-  // then scored grouped by list, best bound first within a list.
-  int32_t* slot_seg = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * kSegPerPass;
-  int32_t* slot_p = slot_seg + kSegPerPass;
+  // The remaining lists, as a stream of segment groups per wave: wave w takes the
+  // lists of rank p0 + w, p0 + w + 4, ... whose list bound does not exceed the K-th
+  // best score and evaluates their groups' bounds 16 at a time (a pass may span
+  // several lists, so that short lists do not leave lanes idle); the segments of
+  // the groups kept are evaluated the same way, 16 at a time, and the segments
+  // kept are scored grouped by list, best bound first within a list.
+  int32_t* gslot = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * (kSegPerPass + kSegSlots);
+  int32_t* gslot_p = gslot + kSegPerPass;
+  int32_t* sslot = gslot_p + kSegPerPass;
+  int32_t* sslot_p = sslot + kSegSlots;
+  // Lower bound of every row's ADC score in each of n <= 16 boxes (box ids[j] of
+  // base, list rank ps[j]): per dimension the squared distance from the query to
+  // the box; the entry of subspace m is a sum of its dimensions' squared residual
+  // differences, each at least that (up to box_bound's rounding allowance). S
+  // boxes share the pass (n rounded up to a power of two), G = 64 / S lanes each;
+  // lane g of a box takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
+  // e0: block 0's subspaces, et: the others (partial sums of the lane).
+  auto box_pass = [&](const uint32_t* __restrict__ base, const int32_t* ids, const int32_t* ps, int n,
+                      int& gl, bool& valid, int& id, int& pp, float& e0, float& et) {
+    gl = 2;  // log2(G)
+    while (gl < 6 && (32 >> gl) >= n) ++gl;
+    const int G = 1 << gl;
+    const int jl = lane >> gl;
+    const int g = lane & (G - 1);
+    valid = jl < n;
+    id = valid ? ids[jl] : 0;
+    pp = valid ? ps[jl] : 0;
+    e0 = 0.f;
+    et = 0.f;
+    if (valid && base) {
+      const uint32_t* __restrict__ box = base + static_cast<size_t>(id) * static_cast<size_t>(box_dims);
+      const int c = (pq_m + G - 1) >> gl;
+      const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
+      if constexpr (FD > 0) {
+        // Sixteen dimensions of box requested at a time, then reduced.
+        constexpr int kBatch = FD >= 16 ? 1 : 16 / FD;
+        for (int mb = g * c; mb < m_end; mb += kBatch) {
+          // Subspaces past the chunk are clamped to its last one (the loads stay
+          // unconditional) and their terms replaced by +0.
+          uint32_t bx[kBatch][FD];
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            const int m = mb + i < m_end ? mb + i : m_end - 1;
+#pragma unroll
+            for (int u = 0; u < FD; ++u) bx[i][u] = box[m * FD + u];
+          }
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            const int m = mb + i < m_end ? mb + i : m_end - 1;
+            float part = 0.f;
+#pragma unroll
+            for (int u = 0; u < FD; ++u) part = part + box_e2(qs[m * FD + u], bx[i][u]);
+            part = mb + i < m_end ? part : 0.f;
+            e0 = e0 + (mb + i < kBlock ? part : 0.f);
+            et = et + (mb + i < kBlock ? 0.f : part);
+          }
+        }
+      } else {
+        for (int m = g * c; m < m_end; ++m) {
+          float part = 0.f;
+          for (int u = 0; u < dsub; ++u) part = part + box_e2(qs[m * dsub + u], box[m * dsub + u]);
+          if (m < kBlock) {
+            e0 = e0 + part;
+          } else {
+            et = et + part;
+          }
+        }
+      }
+    }
+    for (int o = 1; o < G; o <<= 1) {
+      e0 = e0 + __shfl_xor(e0, o, 64);
+      et = et + __shfl_xor(et, o, 64);
+    }
+  };
+
   int sp = p0 + wave;  // next list rank of this wave
-  int s_off = 0;       // segments of list sp already taken
+  int g_off = 0;       // groups of list sp already taken
   int cur_p = -1;      // list whose residual is in resid
   for (;;) {
     refresh();
     int filled = 0;
     while (filled < kSegPerPass && sp < a.P) {
-      const int nseg = t_nseg[sp];
       if (t_rows[sp] <= 0 || (lboxes && t_lbound[sp] > thr_hi)) {
         sp += kWaves;
-        s_off = 0;
+        g_off = 0;
         continue;
       }
-      const int take = kSegPerPass - filled < nseg - s_off ? kSegPerPass - filled : nseg - s_off;
+      const int g0 = t_g0[sp];
+      const int ngrp = t_ngrp[sp];
+      const int take = kSegPerPass - filled < ngrp - g_off ? kSegPerPass - filled : ngrp - g_off;
       if (lane < take) {
-        slot_seg[filled + lane] = t_sg0[sp] + s_off + lane;
-        slot_p[filled + lane] = sp;
+        gslot[filled + lane] = g0 + g_off + lane;
+        gslot_p[filled + lane] = sp;
       }
       filled += take;
-      s_off += take;
-      if (s_off == nseg) {
+      g_off += take;
+      if (g_off == ngrp) {
         sp += kWaves;
-        s_off = 0;
+        g_off = 0;
       }
     }
     if (filled == 0) break;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Group bounds; the segments of the groups kept (in slot order, so lists stay
+    // in rank order) go to the segment slots.
+    int ns = 0;
     {
-      // S segments share this pass, G = 64 / S lanes each (S a power of two).
-      const int remaining = filled;
-      int gl = 2;  // log2(G)
-      while (gl < 6 && (32 >> gl) >= remaining) ++gl;
-      const int G = 1 << gl;
-      const int jl = lane >> gl;
-      const int g = lane & (G - 1);
-      const bool valid = jl < remaining;
-      const int seg = valid ? slot_seg[jl] : 0;
-      const int pp = valid ? slot_p[jl] : 0;
-      // Lower bound of every row's ADC score in the segment: per dimension the
-      // squared distance from the query to the segment's box; the entry of
-      // subspace m is a sum of its dimensions' squared residual differences, each
-      // at least that (up to box_bound's rounding allowance). e0: block 0's
-      // subspaces, et: the others. Lane g of a segment takes the subspaces
-      // [g * c, (g + 1) * c), c = ceil(pq_m / G).
-      float e0 = 0.f, et = 0.f;
-      if (valid && boxes) {
-        const uint32_t* __restrict__ box = boxes + static_cast<size_t>(seg) * static_cast<size_t>(box_dims);
-        const int c = (pq_m + G - 1) >> gl;
-        const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
-        if constexpr (FD > 0) {
-          // Sixteen dimensions of box requested at a time, then reduced.
-          constexpr int kBatch = FD >= 16 ? 1 : 16 / FD;
-          for (int mb = g * c; mb < m_end; mb += kBatch) {
-            // Subspaces past the chunk are clamped to its last one (the loads stay
-            // unconditional) and their terms replaced by +0.
-            uint32_t bx[kBatch][FD];
-#pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-              const int m = mb + i < m_end ? mb + i : m_end - 1;
-#pragma unroll
-              for (int u = 0; u < FD; ++u) bx[i][u] = box[m * FD + u];
-            }
-#pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-              const int m = mb + i < m_end ? mb + i : m_end - 1;
-              float part = 0.f;
-#pragma unroll
-              for (int u = 0; u < FD; ++u) part = part + box_e2(qs[m * FD + u], bx[i][u]);
-              part = mb + i < m_end ? part : 0.f;
-              e0 = e0 + (mb + i < kBlock ? part : 0.f);
-              et = et + (mb + i < kBlock ? 0.f : part);
-            }
-          }
-        } else {
-          for (int m = g * c; m < m_end; ++m) {
-            float part = 0.f;
-            for (int u = 0; u < dsub; ++u) part = part + box_e2(qs[m * dsub + u], box[m * dsub + u]);
-            if (m < kBlock) {
-              e0 = e0 + part;
-            } else {
-              et = et + part;
-            }
-          }
+      int gl, grp, pp;
+      bool valid;
+      float e0, et;
+      box_pass(a.grp_box, gslot, gslot_p, filled, gl, valid, grp, pp, e0, et);
+      const int32_t gs0 = a.grp_seg[grp];
+      const int32_t gs1 = a.grp_seg[grp + 1];
+      const float etot = box_bound(e0 + et, slack, dims_all);
+      refresh();
+      const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && !(etot > thr_hi);
+      for (uint64_t m = __builtin_amdgcn_ballot_w64(lead); m; m &= m - 1) {
+        const int b = __builtin_ctzll(m);
+        const int s0 = __builtin_amdgcn_readlane(gs0, b);
+        const int n1 = __builtin_amdgcn_readlane(gs1, b) - s0;
+        const int n = n1 < OVVS_GROUP_SEGMENTS ? n1 : OVVS_GROUP_SEGMENTS;
+        const int p = __builtin_amdgcn_readlane(pp, b);
+        if (lane < n) {
+          sslot[ns + lane] = s0 + lane;
+          sslot_p[ns + lane] = p;
         }
+        ns += n;
       }
-      for (int o = 1; o < G; o <<= 1) {
-        e0 = e0 + __shfl_xor(e0, o, 64);
-        et = et + __shfl_xor(et, o, 64);
-      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int c0 = 0; c0 < ns; c0 += kSegPerPass) {
+      const int remaining = ns - c0 < kSegPerPass ? ns - c0 : kSegPerPass;
+      int gl, seg, pp;
+      bool valid;
+      float e0, et;
+      box_pass(boxes, sslot + c0, sslot_p + c0, remaining, gl, valid, seg, pp, e0, et);
+      const int g = lane & ((1 << gl) - 1);
       const float etot = box_bound(e0 + et, slack, dims_all);
       const float tb = box_bound(et, slack, dims_tail);
       const float tl = (tb > 0.f ? tb : 0.f) * kBoundDown;
@@ -1059,7 +1112,8 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   const OvvsScanArgs& a = *args;
   if (a.nq <= 0) return hipSuccess;
   if (!a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets || !a.codes ||
-      !a.ids || !a.rord || !a.list_seg || !a.seg_start || !a.seg_len || a.positions <= 0 ||
+      !a.ids || !a.rord || !a.list_seg || !a.seg_start || !a.seg_len || !a.list_grp || !a.grp_seg ||
+      (a.seg_box && !a.grp_box) || a.positions <= 0 ||
       a.positions > 0x7fffffff || !a.out_keys || !a.out_pos || !a.out_count || !a.out_stats ||
       a.nq > 0x7fffffff ||
       a.nlist <= 0 ||

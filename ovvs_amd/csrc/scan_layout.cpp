@@ -16,6 +16,8 @@
 #include <cstring>
 #include <limits>
 #include <thread>
+#include <utility>
+#include <vector>
 
 #include "internal.hpp"
 
@@ -197,25 +199,60 @@ void bisect(const float* X, int D, const std::vector<int32_t>& idx, std::vector<
 }
 
 // Segments of one list: rows (indices into the list) of each segment in list order,
-// segments in depth-first order of the bisection.
-void segment_list(const float* X, int32_t n, int D, int seg_rows,
-                  std::vector<std::vector<int32_t>>& segs) {
+// segments in depth-first order of the bisection; groups[i] is the first segment of
+// group i, a maximal subtree of the bisection holding at most group_segs segments
+// (so a group is a run of consecutive segments with nearby reconstructions).
+void segment_list(const float* X, int32_t n, int D, int seg_rows, int group_segs,
+                  std::vector<std::vector<int32_t>>& segs, std::vector<int32_t>& groups) {
   segs.clear();
-  std::vector<std::vector<int32_t>> stack;
-  stack.emplace_back(static_cast<size_t>(n));
-  for (int32_t i = 0; i < n; ++i) stack.back()[static_cast<size_t>(i)] = i;
+  groups.clear();
+  // The bisection tree, built without recursion (a split may peel off a single row,
+  // so the depth can reach the list's length). Children get larger node ids than
+  // their parent; a node's segments are the consecutive run [first, first + nsegs).
+  struct Node {
+    int32_t left = -1, right = -1, first = 0, nsegs = 0;
+  };
+  std::vector<Node> nodes(1);
+  std::vector<std::pair<std::vector<int32_t>, int32_t>> stack;
+  stack.emplace_back(std::vector<int32_t>(static_cast<size_t>(n)), 0);
+  for (int32_t i = 0; i < n; ++i) stack.back().first[static_cast<size_t>(i)] = i;
   std::vector<int32_t> left, right;
   while (!stack.empty()) {
-    std::vector<int32_t> idx = std::move(stack.back());
+    std::vector<int32_t> idx = std::move(stack.back().first);
+    const int32_t v = stack.back().second;
     stack.pop_back();
     if (static_cast<int>(idx.size()) <= seg_rows) {
       std::sort(idx.begin(), idx.end());
+      nodes[static_cast<size_t>(v)].first = static_cast<int32_t>(segs.size());
+      nodes[static_cast<size_t>(v)].nsegs = 1;
       segs.push_back(std::move(idx));
       continue;
     }
     bisect(X, D, idx, left, right);
-    stack.push_back(right);
-    stack.push_back(left);
+    const int32_t l = static_cast<int32_t>(nodes.size());
+    nodes[static_cast<size_t>(v)].left = l;
+    nodes[static_cast<size_t>(v)].right = l + 1;
+    nodes.resize(nodes.size() + 2);
+    stack.emplace_back(right, l + 1);  // the left subtree is taken first
+    stack.emplace_back(left, l);
+  }
+  for (size_t v = nodes.size(); v-- > 0;) {
+    Node& nd = nodes[v];
+    if (nd.left < 0) continue;
+    nd.first = nodes[static_cast<size_t>(nd.left)].first;
+    nd.nsegs = nodes[static_cast<size_t>(nd.left)].nsegs + nodes[static_cast<size_t>(nd.right)].nsegs;
+  }
+  // Groups: the maximal subtrees with at most group_segs segments, in segment order.
+  std::vector<int32_t> todo{0};
+  while (!todo.empty()) {
+    const Node& nd = nodes[static_cast<size_t>(todo.back())];
+    todo.pop_back();
+    if (nd.nsegs <= group_segs) {
+      groups.push_back(nd.first);
+      continue;
+    }
+    todo.push_back(nd.right);
+    todo.push_back(nd.left);
   }
 }
 
@@ -247,6 +284,7 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
 
   // Pass 1 (parallel): segments of every list.
   std::vector<std::vector<std::vector<int32_t>>> segs(static_cast<size_t>(nlist));
+  std::vector<std::vector<int32_t>> grps(static_cast<size_t>(nlist));
   std::atomic<bool> failed{false};
   for_each_list(nlist, [&](int32_t c) {
     try {
@@ -262,7 +300,8 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
           for (int32_t u = 0; u < dsub; ++u) x[m * dsub + u] = cw[u];
         }
       }
-      segment_list(X.data(), n, D, seg_rows, segs[static_cast<size_t>(c)]);
+      segment_list(X.data(), n, D, seg_rows, OVVS_GROUP_SEGMENTS, segs[static_cast<size_t>(c)],
+                   grps[static_cast<size_t>(c)]);
     } catch (...) {
       failed = true;
     }
@@ -271,10 +310,13 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
 
   // Positions and segment indices.
   out.list_seg.assign(static_cast<size_t>(nlist) + 1, 0);
+  out.list_grp.assign(static_cast<size_t>(nlist) + 1, 0);
   std::vector<int64_t> list_pos(static_cast<size_t>(nlist) + 1, 0);
-  int64_t nseg = 0, pos = 0;
+  int64_t nseg = 0, pos = 0, ngrp = 0;
   for (int32_t c = 0; c < nlist; ++c) {
     out.list_seg[static_cast<size_t>(c)] = static_cast<int32_t>(nseg);
+    out.list_grp[static_cast<size_t>(c)] = static_cast<int32_t>(ngrp);
+    ngrp += static_cast<int64_t>(grps[static_cast<size_t>(c)].size());
     list_pos[static_cast<size_t>(c)] = pos;
     for (const auto& s : segs[static_cast<size_t>(c)]) {
       pos += (static_cast<int64_t>(s.size()) + kT - 1) / kT * kT;
@@ -284,6 +326,9 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
       return OVVS_STATUS_DEVICE_UNAVAILABLE;
   }
   out.list_seg[static_cast<size_t>(nlist)] = static_cast<int32_t>(nseg);
+  out.list_grp[static_cast<size_t>(nlist)] = static_cast<int32_t>(ngrp);
+  out.grp_seg.assign(static_cast<size_t>(ngrp) + 1, static_cast<int32_t>(nseg));
+  out.grp_box.assign(static_cast<size_t>(ngrp) * D, 0u);
   list_pos[static_cast<size_t>(nlist)] = pos;
   out.positions = pos;
   out.box_dims = D;
@@ -306,6 +351,9 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
       lbox[2 * d + 1] = -std::numeric_limits<float>::infinity();
     }
     std::vector<float> boxv(static_cast<size_t>(D) * 2);
+    // Residual-coordinate boxes of this list's segments, for the group boxes.
+    std::vector<float> seg_boxes(segs[static_cast<size_t>(c)].size() * static_cast<size_t>(D) * 2);
+    const int32_t sg_first = out.list_seg[static_cast<size_t>(c)];
     for (const auto& s : segs[static_cast<size_t>(c)]) {
       out.seg_start[static_cast<size_t>(sg)] = static_cast<int32_t>(p);
       out.seg_len[static_cast<size_t>(sg)] = static_cast<int32_t>(s.size());
@@ -349,8 +397,31 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
         lbox[2 * d + 1] = std::max(lbox[2 * d + 1], box[2 * d + 1]);
         packed[d] = ovvs::pack_abs_box_fp16(cen[d], box[2 * d], box[2 * d + 1]);
       }
+      std::copy(box, box + static_cast<size_t>(D) * 2,
+                seg_boxes.begin() + static_cast<std::ptrdiff_t>(sg - sg_first) * D * 2);
       p = (p + kT - 1) / kT * kT;
       ++sg;
+    }
+    // Group boxes: the union of their segments' boxes.
+    {
+      const std::vector<int32_t>& gs = grps[static_cast<size_t>(c)];
+      const float* cen = ix.centroids.data() + static_cast<size_t>(c) * static_cast<size_t>(ix.dim);
+      const int32_t g_first = out.list_grp[static_cast<size_t>(c)];
+      const int32_t nsl = static_cast<int32_t>(segs[static_cast<size_t>(c)].size());
+      for (size_t gi = 0; gi < gs.size(); ++gi) {
+        const int32_t s0 = gs[gi];
+        const int32_t s1 = gi + 1 < gs.size() ? gs[gi + 1] : nsl;
+        out.grp_seg[static_cast<size_t>(g_first) + gi] = sg_first + s0;
+        uint32_t* gp = out.grp_box.data() + (static_cast<size_t>(g_first) + gi) * D;
+        for (int d = 0; d < D; ++d) {
+          float lo = std::numeric_limits<float>::infinity(), hi = -lo;
+          for (int32_t k = s0; k < s1; ++k) {
+            lo = std::min(lo, seg_boxes[(static_cast<size_t>(k) * D + d) * 2]);
+            hi = std::max(hi, seg_boxes[(static_cast<size_t>(k) * D + d) * 2 + 1]);
+          }
+          gp[d] = ovvs::pack_abs_box_fp16(cen[d], lo, hi);
+        }
+      }
     }
     // The list's box contains every segment box (an empty list keeps an empty
     // box; the scan never evaluates it).
