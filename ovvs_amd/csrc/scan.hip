@@ -342,8 +342,8 @@ struct ScanLayout {
   size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
   size_t slot_off;   // per wave: [2][kSegPerPass] int32, the groups of a bound pass and
                      //           their list ranks; [2][kSegSlots], the same for segments
-  size_t table_off;  // [8][P] per probe rank: list, rows, ordinal base, first segment,
-                     //        segments, list bound, first group, groups
+  size_t table_off;  // [7][P] per probe rank: list, rows, ordinal base, first group,
+                     //        groups, list bound, group scored in phase 0 (or -1)
   size_t total;
 };
 
@@ -363,7 +363,7 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
   L.slot_off = L.misc_off + 16;
   L.table_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * (kSegPerPass + kSegSlots) * 4;
-  L.total = L.table_off + 8 * static_cast<size_t>(P) * 4;
+  L.total = L.table_off + 7 * static_cast<size_t>(P) * 4;
   return L;
 }
 
@@ -397,32 +397,28 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* t_list = reinterpret_cast<int32_t*>(smem + L.table_off);
   int32_t* t_rows = t_list + a.P;
   uint32_t* t_ord = reinterpret_cast<uint32_t*>(t_rows + a.P);
-  int32_t* t_sg0 = reinterpret_cast<int32_t*>(t_ord + a.P);
-  int32_t* t_nseg = t_sg0 + a.P;
-  float* t_lbound = reinterpret_cast<float*>(t_nseg + a.P);
-  int32_t* t_g0 = reinterpret_cast<int32_t*>(t_lbound + a.P);
+  int32_t* t_g0 = reinterpret_cast<int32_t*>(t_ord + a.P);
   int32_t* t_ngrp = t_g0 + a.P;
+  float* t_lbound = reinterpret_cast<float*>(t_ngrp + a.P);
+  int32_t* t_p0g = reinterpret_cast<int32_t*>(t_lbound + a.P);
   // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
 
   for (int t = static_cast<int>(threadIdx.x); t < a.dim; t += kThreads) qs[t] = a.queries[q * a.dim + t];
   if (lane == 0) wave_thr[wave] = kNoKey;
   if (threadIdx.x == 0) wave_thr[kWaves] = kNoKey;
-  // Probe table: list, rows, segment and group ranges per rank (an
+  // Probe table: list, rows and group range per rank (an
   // invalid probe id is marked -1 with no rows: the search then fails).
   for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
     const int l = a.probes[q * a.P + t];
     const bool ok = static_cast<uint32_t>(l) < static_cast<uint32_t>(a.nlist);
     const int lv = ok ? l : 0;
-    const int32_t sg0 = a.list_seg[lv];
-    const int32_t nseg = a.list_seg[lv + 1] - sg0;
     t_list[t] = ok ? l : -1;
     t_rows[t] = ok ? static_cast<int32_t>(a.list_offsets[lv + 1] - a.list_offsets[lv]) : 0;
-    t_sg0[t] = sg0;
-    t_nseg[t] = ok ? nseg : 0;
     const int32_t g0 = a.list_grp[lv];
     t_g0[t] = g0;
     t_ngrp[t] = ok ? a.list_grp[lv + 1] - g0 : 0;
+    t_p0g[t] = -1;
   }
   __syncthreads();
   // Largest query coordinate magnitude, for the residual rounding allowance.
@@ -642,13 +638,80 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
   };
 
-  // Phase 0: the nearest lists, until they hold 2K rows (or all of them), are
-  // scored completely by all four waves together (64-row tiles in turn, table
-  // slices of 8 subspaces built in LDS from coalesced codebook reads), so that
-  // every wave starts the rest with a threshold; at the end of the phase the K-th
-  // best key of the union of the four lists is published to every wave. The
-  // slices live in the candidate-buffer and queue area, unused until a chunk's
-  // rows are offered.
+  // Lower bound of every row's ADC score in each of n <= 16 boxes (box ids[j] of
+  // base, list rank ps[j]; or boxes id0 + j of rank p_all when ids is null):
+  // per dimension the squared distance from the query to
+  // the box; the entry of subspace m is a sum of its dimensions' squared residual
+  // differences, each at least that (up to box_bound's rounding allowance). S
+  // boxes share the pass (n rounded up to a power of two), G = 64 / S lanes each;
+  // lane g of a box takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
+  // e0: block 0's subspaces, et: the others (partial sums of the lane).
+  auto box_pass = [&](const uint32_t* __restrict__ base, const int32_t* ids, const int32_t* ps, int id0,
+                      int p_all, int n, int& gl, bool& valid, int& id, int& pp, float& e0, float& et) {
+    gl = 2;  // log2(G)
+    while (gl < 6 && (32 >> gl) >= n) ++gl;
+    const int G = 1 << gl;
+    const int jl = lane >> gl;
+    const int g = lane & (G - 1);
+    valid = jl < n;
+    id = !valid ? 0 : ids ? ids[jl] : id0 + jl;
+    pp = !valid ? 0 : ps ? ps[jl] : p_all;
+    e0 = 0.f;
+    et = 0.f;
+    if (valid && base) {
+      const uint32_t* __restrict__ box = base + static_cast<size_t>(id) * static_cast<size_t>(box_dims);
+      const int c = (pq_m + G - 1) >> gl;
+      const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
+      if constexpr (FD > 0) {
+        // Sixteen dimensions of box requested at a time, then reduced.
+        constexpr int kBatch = FD >= 16 ? 1 : 16 / FD;
+        for (int mb = g * c; mb < m_end; mb += kBatch) {
+          // Subspaces past the chunk are clamped to its last one (the loads stay
+          // unconditional) and their terms replaced by +0.
+          uint32_t bx[kBatch][FD];
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            const int m = mb + i < m_end ? mb + i : m_end - 1;
+#pragma unroll
+            for (int u = 0; u < FD; ++u) bx[i][u] = box[m * FD + u];
+          }
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            const int m = mb + i < m_end ? mb + i : m_end - 1;
+            float part = 0.f;
+#pragma unroll
+            for (int u = 0; u < FD; ++u) part = part + box_e2(qs[m * FD + u], bx[i][u]);
+            part = mb + i < m_end ? part : 0.f;
+            e0 = e0 + (mb + i < kBlock ? part : 0.f);
+            et = et + (mb + i < kBlock ? 0.f : part);
+          }
+        }
+      } else {
+        for (int m = g * c; m < m_end; ++m) {
+          float part = 0.f;
+          for (int u = 0; u < dsub; ++u) part = part + box_e2(qs[m * dsub + u], box[m * dsub + u]);
+          if (m < kBlock) {
+            e0 = e0 + part;
+          } else {
+            et = et + part;
+          }
+        }
+      }
+    }
+    for (int o = 1; o < G; o <<= 1) {
+      e0 = e0 + __shfl_xor(e0, o, 64);
+      et = et + __shfl_xor(et, o, 64);
+    }
+  };
+
+  // Phase 0: in the nearest lists, until they hold 2K rows (or all of them), the
+  // group with the smallest bound is scored completely by all four waves
+  // together (64-row tiles in turn, table slices of 8 subspaces built in LDS from
+  // coalesced codebook reads), so that every wave starts the rest with a
+  // threshold; at the end of the phase the K-th best key of the union of the four
+  // lists is published to every wave. The lists' other groups are left to the
+  // independent phase. The slices live in the candidate-buffer and queue area,
+  // unused until a chunk's rows are offered.
   constexpr int kP0Tiles = 4;  // tiles per wave per chunk
   static_assert(static_cast<size_t>(kBlock) * 256 * 4 <=
                     static_cast<size_t>(kWaves) * (kBufCap * 12 + kQueueCap * 8),
@@ -662,16 +725,46 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     if (rows <= 0) continue;
     const int l = t_list[p];
     ord_base = t_ord[p];
-    const int sg0 = t_sg0[p];
-    const int sgl = sg0 + t_nseg[p] - 1;
+    // The list's group with the smallest bound (ties: the first), by wave 0.
+    int bg = t_g0[p];
+    const int ngrp = t_ngrp[p];
+    if (ngrp > 1) {
+      if (wave == 0) {
+        uint64_t best = kNoKey;
+        for (int j0 = 0; j0 < ngrp; j0 += kSegPerPass) {
+          const int n = ngrp - j0 < kSegPerPass ? ngrp - j0 : kSegPerPass;
+          int gl, grp, pp;
+          bool valid;
+          float e0, et;
+          box_pass(a.grp_box, nullptr, nullptr, bg + j0, p, n, gl, valid, grp, pp, e0, et);
+          const float etot = box_bound(e0 + et, slack, dims_all);
+          uint64_t key = valid && (lane & ((1 << gl) - 1)) == 0
+                             ? (static_cast<uint64_t>(score_key(etot)) << 32) | static_cast<uint32_t>(grp)
+                             : kNoKey;
+#pragma unroll
+          for (int o = 32; o >= 1; o >>= 1) {
+            const uint64_t v = shfl_xor_u64(key, o);
+            key = v < key ? v : key;
+          }
+          best = key < best ? key : best;
+        }
+        if (lane == 0) t_p0g[p] = static_cast<int32_t>(best & 0xffffffffu);
+      }
+      __syncthreads();
+      bg = t_p0g[p];
+    } else if (threadIdx.x == 0) {
+      t_p0g[p] = bg;
+    }
     const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
     for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // The list's segments are consecutive in scan order; padding rows have no
+    // The group's segments are consecutive in scan order; padding rows have no
     // in-list index.
-    const int32_t first = a.seg_start[sg0];
+    const int sgf = a.grp_seg[bg];
+    const int sgl = a.grp_seg[bg + 1] - 1;
+    const int32_t first = a.seg_start[sgf];
     const int ntiles = (a.seg_start[sgl] + ((a.seg_len[sgl] + kTile - 1) & ~(kTile - 1)) - first) / kTile;
     for (int c = 0; c < ntiles; c += kWaves * kP0Tiles) {
       float sc[kP0Tiles];
@@ -769,8 +862,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     refresh();
   }
 
-  // The remaining lists, as a stream of segment groups per wave: wave w takes the
-  // lists of rank p0 + w, p0 + w + 4, ... whose list bound does not exceed the K-th
+  // The rest, as a stream of segment groups per wave: wave w takes the lists of
+  // rank w, w + 4, ... whose list bound does not exceed the K-th
   // best score and evaluates their groups' bounds 16 at a time (a pass may span
   // several lists, so that short lists do not leave lanes idle); the segments of
   // the groups kept are evaluated the same way, 16 at a time, and the segments
@@ -779,72 +872,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* gslot_p = gslot + kSegPerPass;
   int32_t* sslot = gslot_p + kSegPerPass;
   int32_t* sslot_p = sslot + kSegSlots;
-  // Lower bound of every row's ADC score in each of n <= 16 boxes (box ids[j] of
-  // base, list rank ps[j]): per dimension the squared distance from the query to
-  // the box; the entry of subspace m is a sum of its dimensions' squared residual
-  // differences, each at least that (up to box_bound's rounding allowance). S
-  // boxes share the pass (n rounded up to a power of two), G = 64 / S lanes each;
-  // lane g of a box takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
-  // e0: block 0's subspaces, et: the others (partial sums of the lane).
-  auto box_pass = [&](const uint32_t* __restrict__ base, const int32_t* ids, const int32_t* ps, int n,
-                      int& gl, bool& valid, int& id, int& pp, float& e0, float& et) {
-    gl = 2;  // log2(G)
-    while (gl < 6 && (32 >> gl) >= n) ++gl;
-    const int G = 1 << gl;
-    const int jl = lane >> gl;
-    const int g = lane & (G - 1);
-    valid = jl < n;
-    id = valid ? ids[jl] : 0;
-    pp = valid ? ps[jl] : 0;
-    e0 = 0.f;
-    et = 0.f;
-    if (valid && base) {
-      const uint32_t* __restrict__ box = base + static_cast<size_t>(id) * static_cast<size_t>(box_dims);
-      const int c = (pq_m + G - 1) >> gl;
-      const int m_end = (g + 1) * c < pq_m ? (g + 1) * c : pq_m;
-      if constexpr (FD > 0) {
-        // Sixteen dimensions of box requested at a time, then reduced.
-        constexpr int kBatch = FD >= 16 ? 1 : 16 / FD;
-        for (int mb = g * c; mb < m_end; mb += kBatch) {
-          // Subspaces past the chunk are clamped to its last one (the loads stay
-          // unconditional) and their terms replaced by +0.
-          uint32_t bx[kBatch][FD];
-#pragma unroll
-          for (int i = 0; i < kBatch; ++i) {
-            const int m = mb + i < m_end ? mb + i : m_end - 1;
-#pragma unroll
-            for (int u = 0; u < FD; ++u) bx[i][u] = box[m * FD + u];
-          }
-#pragma unroll
-          for (int i = 0; i < kBatch; ++i) {
-            const int m = mb + i < m_end ? mb + i : m_end - 1;
-            float part = 0.f;
-#pragma unroll
-            for (int u = 0; u < FD; ++u) part = part + box_e2(qs[m * FD + u], bx[i][u]);
-            part = mb + i < m_end ? part : 0.f;
-            e0 = e0 + (mb + i < kBlock ? part : 0.f);
-            et = et + (mb + i < kBlock ? 0.f : part);
-          }
-        }
-      } else {
-        for (int m = g * c; m < m_end; ++m) {
-          float part = 0.f;
-          for (int u = 0; u < dsub; ++u) part = part + box_e2(qs[m * dsub + u], box[m * dsub + u]);
-          if (m < kBlock) {
-            e0 = e0 + part;
-          } else {
-            et = et + part;
-          }
-        }
-      }
-    }
-    for (int o = 1; o < G; o <<= 1) {
-      e0 = e0 + __shfl_xor(e0, o, 64);
-      et = et + __shfl_xor(et, o, 64);
-    }
-  };
-
-  int sp = p0 + wave;  // next list rank of this wave
+  int sp = wave;       // next list rank of this wave
   int g_off = 0;       // groups of list sp already taken
   int cur_p = -1;      // list whose residual is in resid
   for (;;) {
@@ -881,12 +909,13 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       int gl, grp, pp;
       bool valid;
       float e0, et;
-      box_pass(a.grp_box, gslot, gslot_p, filled, gl, valid, grp, pp, e0, et);
+      box_pass(a.grp_box, gslot, gslot_p, 0, 0, filled, gl, valid, grp, pp, e0, et);
       const int32_t gs0 = a.grp_seg[grp];
       const int32_t gs1 = a.grp_seg[grp + 1];
+      const int32_t done = t_p0g[pp];  // the group phase 0 scored
       const float etot = box_bound(e0 + et, slack, dims_all);
       refresh();
-      const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && !(etot > thr_hi);
+      const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && grp != done && !(etot > thr_hi);
       for (uint64_t m = __builtin_amdgcn_ballot_w64(lead); m; m &= m - 1) {
         const int b = __builtin_ctzll(m);
         const int s0 = __builtin_amdgcn_readlane(gs0, b);
@@ -908,7 +937,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       int gl, seg, pp;
       bool valid;
       float e0, et;
-      box_pass(boxes, sslot + c0, sslot_p + c0, remaining, gl, valid, seg, pp, e0, et);
+      box_pass(boxes, sslot + c0, sslot_p + c0, 0, 0, remaining, gl, valid, seg, pp, e0, et);
       const int g = lane & ((1 << gl) - 1);
       const float etot = box_bound(e0 + et, slack, dims_all);
       const float tb = box_bound(et, slack, dims_tail);
