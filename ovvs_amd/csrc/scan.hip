@@ -303,6 +303,32 @@ __device__ __forceinline__ float box_e2(float r, uint32_t b) {
   return e * e;
 }
 
+// acc + d^2 for the distance d from r to the range packed in b (one rounding).
+__device__ __forceinline__ float box_acc(float r, uint32_t b, float acc) {
+  const float lo = __half2float(__ushort_as_half(static_cast<uint16_t>(b & 0xffffu)));
+  const float hi = __half2float(__ushort_as_half(static_cast<uint16_t>(b >> 16)));
+  const float e = r - __builtin_amdgcn_fmed3f(r, lo, hi);
+  return __builtin_fmaf(e, e, acc);
+}
+
+// v from another lane of the same row, by a DPP control (quad_perm, row mirrors).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of 2^gl lanes; every lane of a group gets the same value
+// (each step adds two equal partial sums in either order). All lanes active.
+__device__ __forceinline__ float group_sum(float e, int gl) {
+  if (gl >= 1) e = e + dpp_f<0xB1>(e);   // quad_perm(1, 0, 3, 2): lane ^ 1
+  if (gl >= 2) e = e + dpp_f<0x4E>(e);   // quad_perm(2, 3, 0, 1): lane ^ 2
+  if (gl >= 3) e = e + dpp_f<0x141>(e);  // row_half_mirror: the other quad of 8 lanes
+  if (gl >= 4) e = e + dpp_f<0x140>(e);  // row_mirror: the other half of 16 lanes
+  if (gl >= 5) e = e + __shfl_xor(e, 16, 64);
+  if (gl >= 6) e = e + __shfl_xor(e, 32, 64);
+  return e;
+}
+
 // Boxes are stored in absolute coordinates (the list centroid added), so the
 // distance is measured from q rather than from the residual fl(q - c) the table
 // entries use. Rounding moves each residual coordinate by at most s (2^-21 times
@@ -435,50 +461,63 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   const float slack = 0x1p-21f * (qmax + a.box_cmax);
   const float dims_all = static_cast<float>(box_dims);
   const float dims_tail = static_cast<float>(box_dims - mb0 * dsub);
-  // Lower bound of every probed list's scores from its box (all four waves, the
-  // loads of many lists in flight together): the sum over the subspace dimensions
-  // of the squared distance from the residual q - c to the box. A list whose
-  // bound exceeds the K-th best score when its turn comes is skipped without
-  // touching memory.
+  // Squared distance from the query to each of n <= 16 boxes (box ids[j] of base,
+  // or box id0 + j when ids is null; a negative id reads box 0), before
+  // box_bound's allowance. S boxes share the pass (n rounded up to a power of
+  // two), G = 64 / S = 2^gl lanes each; every lane of a box returns its sum.
+  auto box_total = [&](const uint32_t* __restrict__ base, const int32_t* ids, int id0, int n, int& gl,
+                       bool& valid, int& id) -> float {
+    gl = 2;
+    while (gl < 6 && (32 >> gl) >= n) ++gl;
+    const int G = 1 << gl;
+    const int jl = lane >> gl;
+    const int g = lane & (G - 1);
+    valid = jl < n;
+    id = !valid ? 0 : ids ? ids[jl] : id0 + jl;
+    id = id < 0 ? 0 : id;
+    float e = 0.f;
+    if (valid && base) {
+      const uint32_t* __restrict__ box = base + static_cast<size_t>(id) * static_cast<size_t>(box_dims);
+      if constexpr (FD > 0) {
+        // box_dims is a multiple of 8 here: 16-byte chunks of four dimensions,
+        // lane g of a box takes chunks g, g + G, ..., three requested at a time
+        // (chunks past the end read the lane's first one and add +0).
+        const int nch = box_dims >> 2;
+        const uint4* __restrict__ b4 = reinterpret_cast<const uint4*>(box);
+        const float4* q4 = reinterpret_cast<const float4*>(qs);
+        for (int k = g; k < nch; k += 3 * G) {
+          uint4 bx[3];
+#pragma unroll
+          for (int i = 0; i < 3; ++i) bx[i] = b4[k + i * G < nch ? k + i * G : k];
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            const float4 qv = q4[k + i * G < nch ? k + i * G : k];
+            float t = box_acc(qv.x, bx[i].x, 0.f);
+            t = box_acc(qv.y, bx[i].y, t);
+            t = box_acc(qv.z, bx[i].z, t);
+            t = box_acc(qv.w, bx[i].w, t);
+            e = e + (k + i * G < nch ? t : 0.f);
+          }
+        }
+      } else {
+        const int cd = (box_dims + G - 1) >> gl;
+        const int d_end = (g + 1) * cd < box_dims ? (g + 1) * cd : box_dims;
+        for (int d = g * cd; d < d_end; ++d) e = box_acc(qs[d], box[d], e);
+      }
+    }
+    return group_sum(e, gl);
+  };
+  // Lower bound of every probed list's scores from its box (16 lists per wave
+  // pass): the sum over the subspace dimensions of the squared distance from the
+  // residual q - c to the box. A list whose bound exceeds the K-th best score
+  // when its turn comes is skipped without touching memory.
   if (lboxes) {
-    // Wave w takes ranks 8w .. 8w + 7, 8w + 32 .. ; lanes read consecutive
-    // dimensions of a list's box; eight lists and two 64-dimension groups are
-    // requested before the arithmetic.
-    constexpr int kLists = 8;
-    for (int pb = wave * kLists; pb < a.P; pb += kWaves * kLists) {
-      float e[kLists];
-#pragma unroll
-      for (int j = 0; j < kLists; ++j) e[j] = 0.f;
-      for (int d0 = 0; d0 < box_dims; d0 += 128) {
-        uint32_t bx[2][kLists];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int d = d0 + 64 * h + lane < box_dims ? d0 + 64 * h + lane : box_dims - 1;
-#pragma unroll
-          for (int j = 0; j < kLists; ++j) {
-            const int p = pb + j < a.P ? pb + j : a.P - 1;
-            const int l = t_rows[p] > 0 ? t_list[p] : 0;
-            bx[h][j] = lboxes[static_cast<size_t>(l) * static_cast<size_t>(box_dims) + d];
-          }
-        }
-        // Dimensions past box_dims read the last one and contribute +0.
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int d = d0 + 64 * h + lane < box_dims ? d0 + 64 * h + lane : box_dims - 1;
-          const bool in = d0 + 64 * h + lane < box_dims;
-#pragma unroll
-          for (int j = 0; j < kLists; ++j) {
-            const float t = box_e2(qs[d], bx[h][j]);
-            e[j] = e[j] + (in ? t : 0.f);
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kLists; ++j) {
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) e[j] = e[j] + __shfl_xor(e[j], o, 64);
-        if (lane == 0 && pb + j < a.P) t_lbound[pb + j] = box_bound(e[j], slack, dims_all);
-      }
+    for (int pb = wave * kSegPerPass; pb < a.P; pb += kWaves * kSegPerPass) {
+      const int n = a.P - pb < kSegPerPass ? a.P - pb : kSegPerPass;
+      int gl, id;
+      bool valid;
+      const float e = box_total(lboxes, t_list + pb, 0, n, gl, valid, id);
+      if (valid && (lane & ((1 << gl) - 1)) == 0) t_lbound[pb + (lane >> gl)] = box_bound(e, slack, dims_all);
     }
   }
   // Ordinal bases (exclusive prefix sums of the rows) and the end of phase 0:
@@ -638,24 +677,23 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
   };
 
-  // Lower bound of every row's ADC score in each of n <= 16 boxes (box ids[j] of
-  // base, list rank ps[j]; or boxes id0 + j of rank p_all when ids is null):
-  // per dimension the squared distance from the query to
+  // Lower bound of every row's ADC score in each of n <= 16 segment boxes (box
+  // ids[j] of base, list rank ps[j]): per dimension the squared distance from the query to
   // the box; the entry of subspace m is a sum of its dimensions' squared residual
   // differences, each at least that (up to box_bound's rounding allowance). S
   // boxes share the pass (n rounded up to a power of two), G = 64 / S lanes each;
   // lane g of a box takes the subspaces [g * c, (g + 1) * c), c = ceil(pq_m / G).
   // e0: block 0's subspaces, et: the others (partial sums of the lane).
-  auto box_pass = [&](const uint32_t* __restrict__ base, const int32_t* ids, const int32_t* ps, int id0,
-                      int p_all, int n, int& gl, bool& valid, int& id, int& pp, float& e0, float& et) {
+  auto box_pass = [&](const uint32_t* __restrict__ base, const int32_t* ids, const int32_t* ps, int n, int& gl,
+                      bool& valid, int& id, int& pp, float& e0, float& et) {
     gl = 2;  // log2(G)
     while (gl < 6 && (32 >> gl) >= n) ++gl;
     const int G = 1 << gl;
     const int jl = lane >> gl;
     const int g = lane & (G - 1);
     valid = jl < n;
-    id = !valid ? 0 : ids ? ids[jl] : id0 + jl;
-    pp = !valid ? 0 : ps ? ps[jl] : p_all;
+    id = valid ? ids[jl] : 0;
+    pp = valid ? ps[jl] : 0;
     e0 = 0.f;
     et = 0.f;
     if (valid && base) {
@@ -733,11 +771,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         uint64_t best = kNoKey;
         for (int j0 = 0; j0 < ngrp; j0 += kSegPerPass) {
           const int n = ngrp - j0 < kSegPerPass ? ngrp - j0 : kSegPerPass;
-          int gl, grp, pp;
+          int gl, grp;
           bool valid;
-          float e0, et;
-          box_pass(a.grp_box, nullptr, nullptr, bg + j0, p, n, gl, valid, grp, pp, e0, et);
-          const float etot = box_bound(e0 + et, slack, dims_all);
+          const float etot = box_bound(box_total(a.grp_box, nullptr, bg + j0, n, gl, valid, grp), slack, dims_all);
           uint64_t key = valid && (lane & ((1 << gl) - 1)) == 0
                              ? (static_cast<uint64_t>(score_key(etot)) << 32) | static_cast<uint32_t>(grp)
                              : kNoKey;
@@ -906,14 +942,13 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     // in rank order) go to the segment slots.
     int ns = 0;
     {
-      int gl, grp, pp;
+      int gl, grp;
       bool valid;
-      float e0, et;
-      box_pass(a.grp_box, gslot, gslot_p, 0, 0, filled, gl, valid, grp, pp, e0, et);
+      const float etot = box_bound(box_total(a.grp_box, gslot, 0, filled, gl, valid, grp), slack, dims_all);
+      const int pp = valid ? gslot_p[lane >> gl] : 0;
       const int32_t gs0 = a.grp_seg[grp];
       const int32_t gs1 = a.grp_seg[grp + 1];
       const int32_t done = t_p0g[pp];  // the group phase 0 scored
-      const float etot = box_bound(e0 + et, slack, dims_all);
       refresh();
       const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && grp != done && !(etot > thr_hi);
       for (uint64_t m = __builtin_amdgcn_ballot_w64(lead); m; m &= m - 1) {
@@ -937,7 +972,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       int gl, seg, pp;
       bool valid;
       float e0, et;
-      box_pass(boxes, sslot + c0, sslot_p + c0, 0, 0, remaining, gl, valid, seg, pp, e0, et);
+      box_pass(boxes, sslot + c0, sslot_p + c0, remaining, gl, valid, seg, pp, e0, et);
       const int g = lane & ((1 << gl) - 1);
       const float etot = box_bound(e0 + et, slack, dims_all);
       const float tb = box_bound(et, slack, dims_tail);
