@@ -63,6 +63,7 @@ struct ScanLayoutHost {
                                    // binary16 rounded outward, packed lo | hi << 16
   std::vector<uint32_t> list_box;  // [nlist * box_dims] the same over each whole list
   float cmax = 0.f;                // max |centroid coordinate| (+inf if any is not finite)
+  std::vector<int32_t> list_rank;  // [nlist] spatial order of the lists (a permutation)
   std::vector<int64_t> ids;        // [positions] row id, -1 for padding
   std::vector<int32_t> rord;       // [positions] index of the row within its list, -1 padding
   std::vector<uint8_t> codes;      // tiled codes by scan position (kernels.hpp)
@@ -101,6 +102,7 @@ struct IndexDevice {
   DeviceBuffer seg_len;    // [nseg] i32
   DeviceBuffer seg_box;    // [nseg * box_dims] packed binary16 (lo, hi)
   DeviceBuffer list_box;   // [nlist * box_dims] packed binary16 (lo, hi)
+  DeviceBuffer list_rank;  // [nlist] i32 spatial order of the lists
   DeviceBuffer list_grp;   // [nlist + 1] i32
   DeviceBuffer grp_seg;    // [ngrp + 1] i32
   DeviceBuffer grp_box;    // [ngrp * box_dims] packed binary16 (lo, hi)

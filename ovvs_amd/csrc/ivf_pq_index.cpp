@@ -304,6 +304,8 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
     OVVS_TRY(alloc(d->grp_box, std::max<size_t>(lay.grp_box.size(), 1) * 4, work));
     OVVS_TRY(h2d(d->grp_box.get(), lay.grp_box.data(), lay.grp_box.size() * 4, s, work));
   }
+  OVVS_TRY(alloc(d->list_rank, lay.list_rank.size() * 4, work));
+  OVVS_TRY(h2d(d->list_rank.get(), lay.list_rank.data(), lay.list_rank.size() * 4, s, work));
   OVVS_TRY(alloc(d->list_grp, lay.list_grp.size() * 4, work));
   OVVS_TRY(h2d(d->list_grp.get(), lay.list_grp.data(), lay.list_grp.size() * 4, s, work));
   OVVS_TRY(alloc(d->grp_seg, lay.grp_seg.size() * 4, work));

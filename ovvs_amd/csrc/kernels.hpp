@@ -136,6 +136,8 @@ struct OvvsScanArgs {
   const int32_t* list_grp;     // [nlist + 1] group CSR
   const int32_t* grp_seg;      // [ngrp + 1] first segment of each group
   const uint32_t* grp_box;     // [ngrp * pq_m * dsub] the same over each group; or nullptr
+  const int32_t* order;        // [nq] queries in processing order (ovvs_hip_query_order), or
+                               // nullptr for query b in workgroup b
   float box_cmax;              // max |centroid coordinate| (+inf if any is not finite)
   int64_t positions;           // scan positions
   const uint8_t* codes;        // tiled codes by scan position, see OVVS_CODE_TILE_ROWS
@@ -155,6 +157,11 @@ struct OvvsScanArgs {
 // Code scan + per-query shortlist of the K best (ADC score, dense ordinal) rows
 // over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
+// order = the queries 0 .. nq-1 sorted by the spatial rank (list_rank, a permutation
+// of the lists) of their nearest probed list (probes[q * P]); the scan hands each
+// XCD one contiguous part of it, so that its L2 serves lists near each other.
+hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
+                                int32_t nlist, int32_t* order, hipStream_t stream);
 // counters[i] += sum over the queries of stats[q * 4 + i], i < 4 (the scan's
 // per-query statistics).
 hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq, unsigned long long* counters,

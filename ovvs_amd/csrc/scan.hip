@@ -344,6 +344,14 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Position in the query order of workgroup b of n. Workgroups go to the eight XCDs
+// in turn (b to XCD b % 8); XCD x takes the x-th of eight consecutive parts of the
+// order (the first n % 8 parts one longer), in order.
+__device__ __forceinline__ int64_t xcd_slot(int64_t b, int64_t n) {
+  const int64_t x = b & 7, k = b >> 3, m = n >> 3, r = n & 7;
+  return x < r ? x * (m + 1) + k : r * (m + 1) + (x - r) * m + k;
+}
+
 constexpr int kQueueCap = 128;
 // At most this many segments share one bound pass (at least 4 lanes each).
 constexpr int kSegPerPass = 16;
@@ -409,7 +417,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* qpos = reinterpret_cast<int32_t*>(smem + L.qpos_off) + wave * kQueueCap;
   float* qsc = reinterpret_cast<float*>(smem + L.qsc_off) + wave * kQueueCap;
 
-  const int64_t q = blockIdx.x;
+  const int64_t q = a.order ? a.order[xcd_slot(blockIdx.x, a.nq)] : static_cast<int64_t>(blockIdx.x);
   const int ks = a.ks;
   const int K = a.K;
   const int pq_m = a.pq_m;
@@ -1234,6 +1242,63 @@ __global__ __launch_bounds__(256) void k_scan_stats(const int32_t* __restrict__ 
 }
 
 }  // namespace
+
+// Counting sort of the queries by the spatial rank of their nearest list (ranks
+// bucketed to at most 4096 buckets); one workgroup, LDS counters.
+__global__ __launch_bounds__(1024) void k_query_order(const int32_t* __restrict__ probes, int64_t nq, int P,
+                                                      const int32_t* __restrict__ list_rank, int nlist, int shift,
+                                                      int32_t* __restrict__ order) {
+  __shared__ int32_t hist[4096];
+  __shared__ int32_t wsum[16];
+  const int t = static_cast<int>(threadIdx.x);
+  const int lane = lane_id(), wave = t >> 6;
+  auto bucket = [&](int64_t q) {
+    const int l = probes[q * P];
+    return static_cast<uint32_t>(l) < static_cast<uint32_t>(nlist) ? (list_rank[l] >> shift) : 0;
+  };
+  for (int i = t; i < 4096; i += 1024) hist[i] = 0;
+  __syncthreads();
+  for (int64_t q = t; q < nq; q += 1024) atomicAdd(&hist[bucket(q)], 1);
+  __syncthreads();
+  // Exclusive prefix sums of the 4096 counters: four per thread, then across the
+  // lanes of each wave and across the 16 waves.
+  int32_t c[4];
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = hist[4 * t + i];
+    s += c[i];
+  }
+  int32_t incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  base += incl - s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hist[4 * t + i] = base;
+    base += c[i];
+  }
+  __syncthreads();
+  for (int64_t q = t; q < nq; q += 1024) order[atomicAdd(&hist[bucket(q)], 1)] = static_cast<int32_t>(q);
+}
+
+extern "C" hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
+                                           int32_t nlist, int32_t* order, hipStream_t stream) {
+  if (nq <= 0) return hipSuccess;
+  if (!probes || !list_rank || !order || P <= 0 || nlist <= 0 || nq > 0x7fffffff) return hipErrorInvalidValue;
+  int shift = 0;
+  while (((nlist - 1) >> shift) >= 4096) ++shift;
+  hipLaunchKernelGGL(k_query_order, dim3(1), dim3(1024), 0, stream, probes, nq, static_cast<int>(P), list_rank,
+                     static_cast<int>(nlist), shift, order);
+  return hipGetLastError();
+}
 
 extern "C" hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq,
                                           unsigned long long* counters, hipStream_t stream) {

@@ -433,6 +433,27 @@ ovvsStatus make_scan_layout(const ovvsIvfPqIndexImpl& ix, int seg_rows, ScanLayo
                        : 0x7c00fc00u;
     }
   });
+  // Spatial rank of every list: the depth-first order of a recursive 2-means
+  // bisection of the centroids (lists with nearby centroids get nearby ranks).
+  {
+    out.list_rank.assign(static_cast<size_t>(nlist), 0);
+    std::vector<std::vector<int32_t>> stack;
+    stack.emplace_back(static_cast<size_t>(nlist));
+    for (int32_t c = 0; c < nlist; ++c) stack.back()[static_cast<size_t>(c)] = c;
+    std::vector<int32_t> left, right;
+    int32_t next = 0;
+    while (!stack.empty()) {
+      std::vector<int32_t> idx = std::move(stack.back());
+      stack.pop_back();
+      if (idx.size() <= 1) {
+        for (const int32_t c : idx) out.list_rank[static_cast<size_t>(c)] = next++;
+        continue;
+      }
+      bisect(ix.centroids.data(), ix.dim, idx, left, right);
+      stack.push_back(right);
+      stack.push_back(left);
+    }
+  }
   // Largest centroid coordinate magnitude (+inf if any is not finite): bounds how
   // far rounding can move a residual coordinate.
   out.cmax = 0.f;
