@@ -317,6 +317,18 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
 }
 
+// Inclusive prefix sum across the 64 lanes (row shifts within 16 lanes, then row
+// broadcasts; all lanes active). Lanes a shift moves past a row's edge add 0.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // Sum over aligned groups of 2^gl lanes; every lane of a group gets the same value
 // (each step adds two equal partial sums in either order). All lanes active.
 __device__ __forceinline__ float group_sum(float e, int gl) {
@@ -357,6 +369,12 @@ constexpr int kQueueCap = 128;
 constexpr int kSegPerPass = 16;
 // Segment slots of one group pass (every group holds at most OVVS_GROUP_SEGMENTS).
 constexpr int kSegSlots = OVVS_GROUP_SEGMENTS * kSegPerPass;
+// Groups the independent phase holds in LDS at a time.
+constexpr int kItemCap = 256;
+// Phase 0: candidate groups per rank (of the first kWaves ranks) and rounds.
+constexpr int kP0Cand = 64;
+constexpr int kP0Rounds = 4;
+static_assert(kWaves * kP0Cand * 8 <= kWaves * 2 * kSegSlots * 4, "phase-0 candidates must fit the slot area");
 // Rounding allowances of the lower bounds (valid for up to OVVS_MAX_BOX_DIMS box
 // dimensions and as many subspaces): a threshold raised by 2^-10 relative and a
 // tail bound lowered by 2^-10 relative cover every rounding of the bound sums and
@@ -373,11 +391,16 @@ struct ScanLayout {
   size_t query_off;  // the query row [dim_pad]
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
-  size_t misc_off;   // [4] int32: end of phase 0, bad probe flag
-  size_t slot_off;   // per wave: [2][kSegPerPass] int32, the groups of a bound pass and
-                     //           their list ranks; [2][kSegSlots], the same for segments
-  size_t table_off;  // [7][P] per probe rank: list, rows, ordinal base, first group,
-                     //        groups, list bound, group scored in phase 0 (or -1)
+  size_t misc_off;   // [8] int32: end of phase 0, bad probe flag, rows, lists, groups
+                     //     scored in phase 0 (kP0Rounds)
+  size_t slot_off;   // per wave: [2][kSegSlots] int32, the segments of a bound pass and
+                     //           their list ranks; before: phase 0's candidate groups
+                     //           [kWaves * kP0Cand] u64
+  size_t item_off;   // [kItemCap] int32 group ids, then [kItemCap] int16 list ranks
+  size_t table_off;  // [8][P] per probe rank: list, rows, ordinal base, first group,
+                     //        groups, list bound, group scored in phase 0 (or -1), first
+                     //        item within its 64-rank chunk; then one unused word and
+                     //        the first item of every chunk
   size_t total;
 };
 
@@ -395,9 +418,10 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.resid_off = L.query_off + dim_pad * 4;
   L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
-  L.slot_off = L.misc_off + 16;
-  L.table_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * (kSegPerPass + kSegSlots) * 4;
-  L.total = L.table_off + 7 * static_cast<size_t>(P) * 4;
+  L.slot_off = L.misc_off + 32;
+  L.item_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * kSegSlots * 4;
+  L.table_off = L.item_off + static_cast<size_t>(kItemCap) * 6;
+  L.total = L.table_off + (8 * static_cast<size_t>(P) + 1 + (P + 63) / 64) * 4;
   return L;
 }
 
@@ -435,6 +459,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* t_ngrp = t_g0 + a.P;
   float* t_lbound = reinterpret_cast<float*>(t_ngrp + a.P);
   int32_t* t_p0g = reinterpret_cast<int32_t*>(t_lbound + a.P);
+  int32_t* t_item = t_p0g + a.P;
   // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
 
@@ -538,12 +563,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const uint32_t r = t < a.P ? static_cast<uint32_t>(t_rows[t]) : 0u;
       bad |= (t < a.P && t_list[t] < 0) ? 1 : 0;
       tasks_q += __popcll(__ballot(t < a.P && r > 0));
-      uint32_t incl = r;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += v;
-      }
+      const uint32_t incl = static_cast<uint32_t>(wave_incl_scan(static_cast<int32_t>(r)));
       if (t < a.P) t_ord[t] = base + incl - r;
       const uint64_t reach = __ballot(t < a.P && static_cast<uint64_t>(base) + incl >= 2u * static_cast<uint64_t>(K));
       if (p0 < 0 && reach) p0 = c + __builtin_ctzll(reach) + 1;
@@ -765,40 +785,46 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   float* lut32 = reinterpret_cast<float*>(smem + L.bufk_off);
   uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem + L.bufk_off);
   const int ks_log2 = __ffs(ks) - 1;
-  const int p0 = misc[0];
-  for (int p = 0; p < p0; ++p) {
-    const int32_t rows = t_rows[p];
-    if (rows <= 0) continue;
+  // Candidates: the first kP0Cand groups of ranks 0 .. kWaves-1 (wave w evaluates
+  // rank w's) with their bounds, as keys (bound key << 32 | w * kP0Cand + j).
+  uint64_t* p0c = reinterpret_cast<uint64_t*>(smem + L.slot_off);
+  {
+    for (int j = lane; j < kP0Cand; j += 64) p0c[wave * kP0Cand + j] = kNoKey;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int r = wave;
+    const int ngc = r < a.P && t_rows[r] > 0 ? (t_ngrp[r] < kP0Cand ? t_ngrp[r] : kP0Cand) : 0;
+    for (int j0 = 0; j0 < ngc; j0 += kSegPerPass) {
+      const int n = ngc - j0 < kSegPerPass ? ngc - j0 : kSegPerPass;
+      int gl, grp;
+      bool valid;
+      const float etot = box_bound(box_total(a.grp_box, nullptr, t_g0[r] + j0, n, gl, valid, grp), slack, dims_all);
+      if (valid && (lane & ((1 << gl) - 1)) == 0) {
+        const int c = wave * kP0Cand + j0 + (lane >> gl);
+        p0c[c] = (static_cast<uint64_t>(score_key(etot)) << 32) | static_cast<uint32_t>(c);
+      }
+    }
+  }
+  if (threadIdx.x < kP0Rounds) misc[4 + threadIdx.x] = -1;
+  __syncthreads();
+  // Rounds: the candidate with the smallest bound (ties: the first) is scored; a
+  // further round runs while the best remaining candidate's bound does not exceed
+  // the union's K-th best score (a group the rest of the search would score anyway).
+  for (int round = 0; round < kP0Rounds; ++round) {
+    uint64_t best = kNoKey;
+    for (int k = lane; k < kWaves * kP0Cand; k += 64) best = p0c[k] < best ? p0c[k] : best;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t v = shfl_xor_u64(best, o);
+      best = v < best ? v : best;
+    }
+    if (best == kNoKey || (round > 0 && key_score(best) > thr_hi)) break;
+    const int ck = static_cast<int>(best & 0xffffffffu);
+    const int p = ck / kP0Cand;
+    const int bg = t_g0[p] + ck % kP0Cand;
     const int l = t_list[p];
     ord_base = t_ord[p];
-    // The list's group with the smallest bound (ties: the first), by wave 0.
-    int bg = t_g0[p];
-    const int ngrp = t_ngrp[p];
-    if (ngrp > 1) {
-      if (wave == 0) {
-        uint64_t best = kNoKey;
-        for (int j0 = 0; j0 < ngrp; j0 += kSegPerPass) {
-          const int n = ngrp - j0 < kSegPerPass ? ngrp - j0 : kSegPerPass;
-          int gl, grp;
-          bool valid;
-          const float etot = box_bound(box_total(a.grp_box, nullptr, bg + j0, n, gl, valid, grp), slack, dims_all);
-          uint64_t key = valid && (lane & ((1 << gl) - 1)) == 0
-                             ? (static_cast<uint64_t>(score_key(etot)) << 32) | static_cast<uint32_t>(grp)
-                             : kNoKey;
-#pragma unroll
-          for (int o = 32; o >= 1; o >>= 1) {
-            const uint64_t v = shfl_xor_u64(key, o);
-            key = v < key ? v : key;
-          }
-          best = key < best ? key : best;
-        }
-        if (lane == 0) t_p0g[p] = static_cast<int32_t>(best & 0xffffffffu);
-      }
-      __syncthreads();
-      bg = t_p0g[p];
-    } else if (threadIdx.x == 0) {
-      t_p0g[p] = bg;
-    }
     const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * a.dim;
     for (int t = lane; t < a.dim; t += 64) resid[t] = qs[t] - cv[t];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -873,12 +899,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       }
       settle();
     }
-  }
-  {
-    // Every wave has folded its phase-0 candidates; wave 0 merges copies of the
+    // Every wave has folded this round's candidates; wave 0 merges copies of the
     // four lists and publishes the K-th key of the union.
     constexpr int M = 64 * KPL;
     __syncthreads();
+    if (threadIdx.x == 0) {
+      p0c[ck] = kNoKey;
+      misc[4 + round] = bg;
+    }
     uint64_t* mk = reinterpret_cast<uint64_t*>(smem);
 #pragma unroll
     for (int j = 0; j < KPL; ++j) mk[wave * M + j * 64 + lane] = lk[j];
@@ -906,67 +934,81 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     refresh();
   }
 
-  // The rest, as a stream of segment groups per wave: wave w takes the lists of
-  // rank w, w + 4, ... whose list bound does not exceed the K-th
-  // best score and evaluates their groups' bounds 16 at a time (a pass may span
-  // several lists, so that short lists do not leave lanes idle); the segments of
-  // the groups kept are evaluated the same way, 16 at a time, and the segments
-  // kept are scored grouped by list, best bound first within a list.
-  int32_t* gslot = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * (kSegPerPass + kSegSlots);
-  int32_t* gslot_p = gslot + kSegPerPass;
-  int32_t* sslot = gslot_p + kSegPerPass;
+  // The rest: the items are the groups of every probed list whose list bound does
+  // not exceed the K-th best score, in rank order (the groups phase 0 scored are
+  // passed over). They are dealt to the waves 16 at a time (pass j of wave w takes items
+  // 64 j + 16 w onwards), up to kItemCap per round; the segments of the groups
+  // whose bound does not exceed the K-th best are evaluated the same way, 16 at a
+  // time, and the segments kept are scored grouped by list, best bound first within
+  // a list.
+  int32_t p0done[kP0Rounds];  // groups phase 0 scored (-1: none)
+#pragma unroll
+  for (int r = 0; r < kP0Rounds; ++r) p0done[r] = misc[4 + r];
+  int32_t* sslot = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * kSegSlots;
   int32_t* sslot_p = sslot + kSegSlots;
-  int sp = wave;       // next list rank of this wave
-  int g_off = 0;       // groups of list sp already taken
-  int cur_p = -1;      // list whose residual is in resid
-  for (;;) {
-    refresh();
-    int filled = 0;
-    while (filled < kSegPerPass && sp < a.P) {
-      if (t_rows[sp] <= 0 || (lboxes && t_lbound[sp] > thr_hi)) {
-        sp += kWaves;
-        g_off = 0;
-        continue;
-      }
-      const int g0 = t_g0[sp];
-      const int ngrp = t_ngrp[sp];
-      const int take = kSegPerPass - filled < ngrp - g_off ? kSegPerPass - filled : ngrp - g_off;
-      if (lane < take) {
-        gslot[filled + lane] = g0 + g_off + lane;
-        gslot_p[filled + lane] = sp;
-      }
-      filled += take;
-      g_off += take;
-      if (g_off == ngrp) {
-        sp += kWaves;
-        g_off = 0;
+  int32_t* it_grp = reinterpret_cast<int32_t*>(smem + L.item_off);
+  int16_t* it_rank = reinterpret_cast<int16_t*>(it_grp + kItemCap);
+  // Item counts per rank and their prefix sums: wave w takes the 64-rank chunks
+  // w, w + 4, ... (one rank per lane), chunk totals meet in LDS.
+  int32_t* chunk_tot = t_item + a.P + 1;
+  const int nchunk = (a.P + 63) >> 6;
+  for (int c = wave; c < nchunk; c += kWaves) {
+    const int t = 64 * c + lane;
+    int32_t n = 0;
+    if (t < a.P && t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi)) n = t_ngrp[t];
+    const int32_t incl = wave_incl_scan(n);
+    if (t < a.P) t_item[t] = incl - n;  // within the chunk
+    if (lane == 63) chunk_tot[c] = incl;
+  }
+  __syncthreads();
+  // First item of every chunk (at most 64 chunks: lane c holds chunk c's), in every wave.
+  const int32_t ctot = lane < nchunk ? chunk_tot[lane] : 0;
+  const int32_t cincl = wave_incl_scan(ctot);
+  const int32_t cexcl = cincl - ctot;
+  const int32_t n_items = __builtin_amdgcn_readlane(cincl, 63);
+  int cur_p = -1;  // list whose residual is in resid
+  for (int ib = 0; ib < n_items; ib += kItemCap) {
+    const int nb = n_items - ib < kItemCap ? n_items - ib : kItemCap;
+    // Items [ib, ib + nb) into LDS, each rank's by one lane.
+    for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
+      const int o0 = __builtin_amdgcn_readlane(cexcl, __builtin_amdgcn_readfirstlane(t >> 6)) + t_item[t];
+      const bool alive = t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi);
+      const int cnt = alive ? t_ngrp[t] : 0;
+      const int g0 = t_g0[t];
+      const int j0 = ib - o0 > 0 ? ib - o0 : 0;
+      const int j1 = ib + nb - o0 < cnt ? ib + nb - o0 : cnt;
+      for (int j = j0; j < j1; ++j) {
+        it_grp[o0 + j - ib] = g0 + j;
+        it_rank[o0 + j - ib] = static_cast<int16_t>(t);
       }
     }
-    if (filled == 0) break;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Group bounds; the segments of the groups kept (in slot order, so lists stay
+    __syncthreads();
+    for (int s0 = wave * kSegPerPass; s0 < nb; s0 += kWaves * kSegPerPass) {
+    const int filled = nb - s0 < kSegPerPass ? nb - s0 : kSegPerPass;
+    refresh();
+    // Group bounds; the segments of the groups kept (in item order, so lists stay
     // in rank order) go to the segment slots.
     int ns = 0;
     {
       int gl, grp;
       bool valid;
-      const float etot = box_bound(box_total(a.grp_box, gslot, 0, filled, gl, valid, grp), slack, dims_all);
-      const int pp = valid ? gslot_p[lane >> gl] : 0;
+      const float etot = box_bound(box_total(a.grp_box, it_grp + s0, 0, filled, gl, valid, grp), slack, dims_all);
+      const int pp = valid ? static_cast<int>(it_rank[s0 + (lane >> gl)]) : 0;
       const int32_t gs0 = a.grp_seg[grp];
       const int32_t gs1 = a.grp_seg[grp + 1];
-      const int32_t done = t_p0g[pp];  // the group phase 0 scored
       refresh();
-      const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && grp != done && !(etot > thr_hi);
+      bool done = false;
+#pragma unroll
+      for (int r = 0; r < kP0Rounds; ++r) done |= grp == p0done[r];
+      const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && !done && !(etot > thr_hi);
       for (uint64_t m = __builtin_amdgcn_ballot_w64(lead); m; m &= m - 1) {
         const int b = __builtin_ctzll(m);
-        const int s0 = __builtin_amdgcn_readlane(gs0, b);
-        const int n1 = __builtin_amdgcn_readlane(gs1, b) - s0;
+        const int sg = __builtin_amdgcn_readlane(gs0, b);
+        const int n1 = __builtin_amdgcn_readlane(gs1, b) - sg;
         const int n = n1 < OVVS_GROUP_SEGMENTS ? n1 : OVVS_GROUP_SEGMENTS;
         const int p = __builtin_amdgcn_readlane(pp, b);
         if (lane < n) {
-          sslot[ns + lane] = s0 + lane;
+          sslot[ns + lane] = sg + lane;
           sslot_p[ns + lane] = p;
         }
         ns += n;
@@ -1002,7 +1044,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       const int nkept = __popcll(kept);
       for (int r = 0; r < nkept; ++r) {
         const int b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lead && rank == r));
-        // The threshold may have dropped since the pass.
+        // The threshold may have dropped since the pass (this wave's or another's).
+        refresh();
         if (readlane_f(etot, b) > thr_hi) continue;
         const float tl_j = readlane_f(tl, b);
         const int gs = __builtin_amdgcn_readlane(seg, b);
@@ -1070,8 +1113,13 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
             }
           }
         }
+        // Complete and publish at once, so that every wave prunes with the rows
+        // scored so far.
+        settle();
       }
     }
+    }
+    __syncthreads();  // every wave is done with this round's items
   }
   settle();
 
