@@ -778,7 +778,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // lists is published to every wave. The lists' other groups are left to the
   // independent phase. The slices live in the candidate-buffer and queue area,
   // unused until a chunk's rows are offered.
-  constexpr int kP0Tiles = 4;  // tiles per wave per chunk
+  constexpr int kP0Tiles = 2;  // tiles per wave per chunk (a group holds at most 8 tiles)
   static_assert(static_cast<size_t>(kBlock) * 256 * 4 <=
                     static_cast<size_t>(kWaves) * (kBufCap * 12 + kQueueCap * 8),
                 "table slice must fit the candidate buffers and survivor queues");
@@ -853,6 +853,18 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       for (int b = 0; b < nblocks; ++b) {
         const int m0 = b * kBlock;
         const int mb = pq_m - m0 < kBlock ? pq_m - m0 : kBlock;
+        // This block's code words, requested before the slice is built.
+        uint2 wq[kP0Tiles];
+#pragma unroll
+        for (int i = 0; i < kP0Tiles; ++i) {
+          const int tile = c + wave + kWaves * i;
+          wq[i] = make_uint2(0u, 0u);
+          if (ok[i]) {
+            wq[i] = *reinterpret_cast<const uint2*>(a.codes +
+                                                    static_cast<size_t>((first >> 6) + tile) * tile_bytes +
+                                                    b * (kTile * kBlock) + lane * kBlock);
+          }
+        }
         __syncthreads();  // every wave is done with the previous slice (or buffers)
         if (FD > 0) {
           build_slice_256<(FD > 0 ? FD : 1), F16>(resid, a.codebooks, m0, lut32, lut16);
@@ -864,13 +876,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         for (int i = 0; i < kP0Tiles; ++i) {
           const int tile = c + wave + kWaves * i;
           if (tile >= ntiles) continue;
-          uint2 w = make_uint2(0u, 0u);
-          if (ok[i]) {
-            w = *reinterpret_cast<const uint2*>(a.codes +
-                                                static_cast<size_t>((first >> 6) + tile) * tile_bytes +
-                                                b * (kTile * kBlock) + lane * kBlock);
-          }
-          const uint32_t wv[2] = {w.x, w.y};
+          const uint32_t wv[2] = {wq[i].x, wq[i].y};
           float acc = sc[i];
           if (FD > 0) {
             float v[kBlock];
