@@ -139,7 +139,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     need += align256(static_cast<size_t>(nq) * 4);                        // query norms
     need += align256(static_cast<size_t>(nq) * P * 4);                    // probes
     need += align256(static_cast<size_t>(nq) * 4);                        // probe fallback flags
-    need += align256(static_cast<size_t>(nq) * 4);                        // scan query order
+    need += 2 * align256(static_cast<size_t>(nq) * 4);                    // scan query order, keys
     need += align256(static_cast<size_t>(qc) * ix.nlist * 4);             // score chunk
     need += align256(static_cast<size_t>(nq) * R * 8);                    // shortlist keys
     need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
@@ -159,6 +159,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     int32_t* d_probes = cv.take<int32_t>(static_cast<size_t>(nq) * P);
     int32_t* d_flags = cv.take<int32_t>(static_cast<size_t>(nq));
     int32_t* d_order = cv.take<int32_t>(static_cast<size_t>(nq));
+    int32_t* d_okeys = cv.take<int32_t>(static_cast<size_t>(nq));
     float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
     uint64_t* d_skeys = cv.take<uint64_t>(static_cast<size_t>(nq) * R);
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
@@ -229,7 +230,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       }
     }
     SEARCH_HIP(hipEventRecord(ev[2], s));
-    SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_order, s));
+    SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_okeys, d_order, s));
 
     OvvsScanArgs sa{};
     sa.queries = d_q;
@@ -290,7 +291,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.invalid = d_counters + 3;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += 5 + 2 * chunks;
+    work.kernel_launches += 6 + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

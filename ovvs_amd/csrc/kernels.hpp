@@ -160,8 +160,9 @@ hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
 // order = the queries 0 .. nq-1 sorted by the spatial rank (list_rank, a permutation
 // of the lists) of their nearest probed list (probes[q * P]); the scan hands each
 // XCD one contiguous part of it, so that its L2 serves lists near each other.
+// keys: [nq] workspace.
 hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
-                                int32_t nlist, int32_t* order, hipStream_t stream);
+                                int32_t nlist, int32_t* keys, int32_t* order, hipStream_t stream);
 // counters[i] += sum over the queries of stats[q * 4 + i], i < 4 (the scan's
 // per-query statistics).
 hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq, unsigned long long* counters,

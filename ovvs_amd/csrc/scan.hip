@@ -1297,22 +1297,29 @@ __global__ __launch_bounds__(256) void k_scan_stats(const int32_t* __restrict__ 
 
 }  // namespace
 
-// Counting sort of the queries by the spatial rank of their nearest list (ranks
-// bucketed to at most 4096 buckets); one workgroup, LDS counters.
-__global__ __launch_bounds__(1024) void k_query_order(const int32_t* __restrict__ probes, int64_t nq, int P,
-                                                      const int32_t* __restrict__ list_rank, int nlist, int shift,
-                                                      int32_t* __restrict__ order) {
+// Bucket of every query: the spatial rank of its nearest probed list, shifted to at
+// most 4096 buckets (bucket 0 for an invalid probe id).
+__global__ __launch_bounds__(256) void k_query_keys(const int32_t* __restrict__ probes, int64_t nq, int P,
+                                                    const int32_t* __restrict__ list_rank, int nlist, int shift,
+                                                    int32_t* __restrict__ keys) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (q >= nq) return;
+  const int l = probes[q * P];
+  const bool in = static_cast<uint32_t>(l) < static_cast<uint32_t>(nlist);
+  keys[q] = in ? (list_rank[l] >> shift) : 0;
+}
+
+// Counting sort of the queries by bucket; one workgroup, LDS counters.
+constexpr int kOrderThreads = 1024;
+__global__ __launch_bounds__(kOrderThreads) void k_query_order(const int32_t* __restrict__ keys, int64_t nq,
+                                                               int32_t* __restrict__ order) {
   __shared__ int32_t hist[4096];
-  __shared__ int32_t wsum[16];
+  __shared__ int32_t wsum[kOrderThreads / 64];
   const int t = static_cast<int>(threadIdx.x);
   const int lane = lane_id(), wave = t >> 6;
-  auto bucket = [&](int64_t q) {
-    const int l = probes[q * P];
-    return static_cast<uint32_t>(l) < static_cast<uint32_t>(nlist) ? (list_rank[l] >> shift) : 0;
-  };
-  for (int i = t; i < 4096; i += 1024) hist[i] = 0;
+  for (int i = t; i < 4096; i += kOrderThreads) hist[i] = 0;
   __syncthreads();
-  for (int64_t q = t; q < nq; q += 1024) atomicAdd(&hist[bucket(q)], 1);
+  for (int64_t q = t; q < nq; q += kOrderThreads) atomicAdd(&hist[keys[q]], 1);
   __syncthreads();
   // Exclusive prefix sums of the 4096 counters: four per thread, then across the
   // lanes of each wave and across the 16 waves.
@@ -1323,12 +1330,7 @@ __global__ __launch_bounds__(1024) void k_query_order(const int32_t* __restrict_
     c[i] = hist[4 * t + i];
     s += c[i];
   }
-  int32_t incl = s;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int32_t v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
-  }
+  const int32_t incl = wave_incl_scan(s);
   if (lane == 63) wsum[wave] = incl;
   __syncthreads();
   int32_t base = 0;
@@ -1340,17 +1342,19 @@ __global__ __launch_bounds__(1024) void k_query_order(const int32_t* __restrict_
     base += c[i];
   }
   __syncthreads();
-  for (int64_t q = t; q < nq; q += 1024) order[atomicAdd(&hist[bucket(q)], 1)] = static_cast<int32_t>(q);
+  for (int64_t q = t; q < nq; q += kOrderThreads) order[atomicAdd(&hist[keys[q]], 1)] = static_cast<int32_t>(q);
 }
 
 extern "C" hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
-                                           int32_t nlist, int32_t* order, hipStream_t stream) {
+                                           int32_t nlist, int32_t* keys, int32_t* order, hipStream_t stream) {
   if (nq <= 0) return hipSuccess;
-  if (!probes || !list_rank || !order || P <= 0 || nlist <= 0 || nq > 0x7fffffff) return hipErrorInvalidValue;
+  if (!probes || !list_rank || !keys || !order || P <= 0 || nlist <= 0 || nq > 0x7fffffff)
+    return hipErrorInvalidValue;
   int shift = 0;
   while (((nlist - 1) >> shift) >= 4096) ++shift;
-  hipLaunchKernelGGL(k_query_order, dim3(1), dim3(1024), 0, stream, probes, nq, static_cast<int>(P), list_rank,
-                     static_cast<int>(nlist), shift, order);
+  hipLaunchKernelGGL(k_query_keys, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256), 0, stream, probes, nq,
+                     static_cast<int>(P), list_rank, static_cast<int>(nlist), shift, keys);
+  hipLaunchKernelGGL(k_query_order, dim3(1), dim3(kOrderThreads), 0, stream, keys, nq, order);
   return hipGetLastError();
 }
 
