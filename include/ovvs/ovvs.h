@@ -74,7 +74,8 @@ typedef struct ovvsIvfPqIndexImpl* ovvsIvfPqIndex_t;
  * Frozen 200-byte layout (reference include/ovvs/ovvs.h:89-121); counters
  * saturate at INT64_MAX. Stage times come from HIP events on the Resources
  * stream: coarse_pairwise_ns is the coarse distance kernel, coarse_topk_ns the
- * probe selection, adc_scan_select_ns the fused LUT-build + code-scan +
+ * probe selection (with the ordering of the queries for the scan),
+ * adc_scan_select_ns the fused LUT-build + code-scan +
  * shortlist kernel (lut_build_ns stays 0 because the LUT is built inside that
  * kernel), refine_distance_ns the fused gather + exact distance + final select
  * kernel. candidate_rows counts every (query, probed list) row scanned, so

@@ -229,8 +229,10 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
         ++chunks;
       }
     }
-    SEARCH_HIP(hipEventRecord(ev[2], s));
+    // The scan's query order (counted in the probe-selection stage, so that the scan
+    // stage times the scan kernel alone).
     SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_okeys, d_order, s));
+    SEARCH_HIP(hipEventRecord(ev[2], s));
 
     OvvsScanArgs sa{};
     sa.queries = d_q;
