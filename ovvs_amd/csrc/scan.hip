@@ -398,9 +398,9 @@ struct ScanLayout {
                      //           [kWaves * kP0Cand] u64
   size_t item_off;   // [kItemCap] int32 group ids, then [kItemCap] int16 list ranks
   size_t table_off;  // [8][P] per probe rank: list, rows, ordinal base, first group,
-                     //        groups, list bound, group scored in phase 0 (or -1), first
-                     //        item within its 64-rank chunk; then one unused word and
-                     //        the first item of every chunk
+                     //        groups, list bound, items (groups of the list if its bound
+                     //        passed), first item within its 64-rank chunk; then one
+                     //        unused word and the first item of every chunk
   size_t total;
 };
 
@@ -458,8 +458,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   int32_t* t_g0 = reinterpret_cast<int32_t*>(t_ord + a.P);
   int32_t* t_ngrp = t_g0 + a.P;
   float* t_lbound = reinterpret_cast<float*>(t_ngrp + a.P);
-  int32_t* t_p0g = reinterpret_cast<int32_t*>(t_lbound + a.P);
-  int32_t* t_item = t_p0g + a.P;
+  int32_t* t_icnt = reinterpret_cast<int32_t*>(t_lbound + a.P);
+  int32_t* t_item = t_icnt + a.P;
   // Bytes of one 64-row code tile.
   const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
 
@@ -477,7 +477,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     const int32_t g0 = a.list_grp[lv];
     t_g0[t] = g0;
     t_ngrp[t] = ok ? a.list_grp[lv + 1] - g0 : 0;
-    t_p0g[t] = -1;
   }
   __syncthreads();
   // Largest query coordinate magnitude, for the residual rounding allowance.
@@ -963,7 +962,10 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     int32_t n = 0;
     if (t < a.P && t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi)) n = t_ngrp[t];
     const int32_t incl = wave_incl_scan(n);
-    if (t < a.P) t_item[t] = incl - n;  // within the chunk
+    if (t < a.P) {
+      t_item[t] = incl - n;  // within the chunk
+      t_icnt[t] = n;         // the rounds below use these counts, whatever the threshold is then
+    }
     if (lane == 63) chunk_tot[c] = incl;
   }
   __syncthreads();
@@ -978,8 +980,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     // Items [ib, ib + nb) into LDS, each rank's by one lane.
     for (int t = static_cast<int>(threadIdx.x); t < a.P; t += kThreads) {
       const int o0 = __builtin_amdgcn_readlane(cexcl, __builtin_amdgcn_readfirstlane(t >> 6)) + t_item[t];
-      const bool alive = t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi);
-      const int cnt = alive ? t_ngrp[t] : 0;
+      const int cnt = t_icnt[t];
       const int g0 = t_g0[t];
       const int j0 = ib - o0 > 0 ? ib - o0 : 0;
       const int j1 = ib + nb - o0 < cnt ? ib + nb - o0 : cnt;

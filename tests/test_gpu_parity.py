@@ -231,6 +231,31 @@ def test_far_from_origin_data_against_oracle(ovvs, res, tmp_path):
     ix.close()
 
 
+def test_many_groups_and_odd_batches_against_oracle(ovvs, res, tmp_path):
+    """Four lists of about 60,000 rows hold hundreds of segment groups each, so one
+    query's groups exceed what the scan holds in LDS at a time (several item
+    rounds) and phase 0's per-list candidate cap; batches of 1, 7 and 13 queries
+    take the XCD-aware query order with a batch that is not a multiple of 8."""
+    rng = np.random.default_rng(41)
+    dim, n = 16, 240000
+    centers = rng.standard_normal((64, dim)).astype(np.float32)
+    data = (centers[rng.integers(0, 64, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=4, pq_m=8, pq_nbits=8, resources=res)
+    p = tmp_path / "groups.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    assert min(len(l) for l in orc.ix.lists) > 20000
+    for nq in (1, 7, 13, 64):
+        q = (centers[rng.integers(0, 64, nq)] + 0.3 * rng.standard_normal((nq, dim))).astype(np.float32)
+        for k, nprobe, krefine in [(10, 4, 10), (10, 3, 32), (100, 4, 100)]:
+            say("nq", nq, "k", k, "nprobe", nprobe)
+            ids, d = ix.search(q, k, nprobe, krefine)
+            oids, od = orc.search(q, k, nprobe, krefine)
+            assert_results_match(ids, d, oids, od, label=f"nq{nq} k{k} p{nprobe}")
+            assert np.array_equal(_bits(d), _bits(od)), f"nq{nq} k{k} p{nprobe}"
+    ix.close()
+
+
 def test_device_pointer_entry_matches_host_entry(ovvs, res, ref_cases, tmp_path):
     import torch
 
