@@ -60,11 +60,24 @@ constexpr int kTile = OVVS_CODE_TILE_ROWS;   // rows per code tile (64)
 
 __host__ __device__ constexpr size_t round16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
 
+// v of lane (this lane ^ s): DPP within 16-lane rows for s = 1, 2 (quad_perm) and
+// 8 (row_ror:8), a cross-lane permute otherwise. s is a constant after unrolling;
+// all lanes active.
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int s) {
+  switch (s) {
+    case 1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xf, 0xf, false));
+    case 2: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xf, 0xf, false));
+    case 8: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false));
+    default: return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), s, 64));
+  }
+}
+
 // Compare-exchange of (k, p) with the lane `s` away; this lane keeps the
 // smaller key when keep_min.
 __device__ __forceinline__ void cx_lane(uint64_t& k, int32_t& p, int s, bool keep_min) {
-  const uint64_t ok = shfl_xor_u64(k, s);
-  const int32_t op = __shfl_xor(p, s, 64);
+  const uint64_t ok = (static_cast<uint64_t>(xor_lane(static_cast<uint32_t>(k >> 32), s)) << 32) |
+                      xor_lane(static_cast<uint32_t>(k), s);
+  const int32_t op = static_cast<int32_t>(xor_lane(static_cast<uint32_t>(p), s));
   const bool take = keep_min ? (ok < k) : (ok > k);
   if (take) {
     k = ok;
@@ -137,7 +150,9 @@ __device__ __forceinline__ uint64_t kth_key(const uint64_t (&lk)[KPL], int K) {
   uint64_t v = lk[0];
 #pragma unroll
   for (int r = 1; r < KPL; ++r) v = (r == j) ? lk[r] : v;
-  return shfl_u64(v, (K - 1) & 63);
+  const int l = __builtin_amdgcn_readfirstlane((K - 1) & 63);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l))) << 32) |
+         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
 }
 
 // Inserts one key (wave-uniform) into the sorted list, dropping the largest.
