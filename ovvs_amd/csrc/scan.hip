@@ -60,16 +60,44 @@ constexpr int kTile = OVVS_CODE_TILE_ROWS;   // rows per code tile (64)
 
 __host__ __device__ constexpr size_t round16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
 
-// v of lane (this lane ^ s): DPP within 16-lane rows for s = 1, 2 (quad_perm) and
-// 8 (row_ror:8), a cross-lane permute otherwise. s is a constant after unrolling;
-// all lanes active.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+}
+
+// v of lane (this lane ^ s), all in VALU: within 16-lane rows by DPP (quad_perm for
+// s = 1, 2; row rotations, where lane i reads lane i - n, for s = 4, 8), across rows
+// by the gfx950 row swaps (v_permlane16_swap / v_permlane32_swap with both operands
+// v: the first result holds the even rows (lower half) twice, the second the odd rows
+// (upper half)). s is a constant after unrolling; all lanes active.
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int s) {
   switch (s) {
-    case 1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xf, 0xf, false));
-    case 2: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xf, 0xf, false));
-    case 8: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false));
+    case 1: return dpp_u<0xB1>(v);
+    case 2: return dpp_u<0x4E>(v);
+    case 4: {
+      // Both rotations run on all lanes and are blended by a lane mask (a select the
+      // compiler may turn into a branch would run each rotation with its source
+      // lanes off).
+      const uint32_t down = dpp_u<0x124>(v), up = dpp_u<0x12C>(v);
+      const uint32_t m = 0u - ((static_cast<uint32_t>(lane_id()) >> 2) & 1u);
+      return (down & m) | (up & ~m);
+    }
+    case 8: return dpp_u<0x128>(v);
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane_id() & 16) ? r[0] : r[1];
+    }
+    case 32: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane_id() & 32) ? r[0] : r[1];
+    }
     default: return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), s, 64));
   }
+}
+
+// v of lane 63 - this lane (row_mirror reverses each 16-lane row, then the rows swap).
+__device__ __forceinline__ uint32_t rev_lane(uint32_t v) {
+  return xor_lane(xor_lane(dpp_u<0x140>(v), 16), 32);
 }
 
 // Compare-exchange of (k, p) with the lane `s` away; this lane keeps the
@@ -134,8 +162,9 @@ template <int KPL>
 __device__ __forceinline__ void merge64(uint64_t (&lk)[KPL], int32_t (&lp)[KPL], uint64_t bk,
                                         int32_t bp) {
   const int lane = lane_id();
-  const uint64_t rk = shfl_u64(bk, 63 - lane);
-  const int32_t rp = __shfl(bp, 63 - lane, 64);
+  const uint64_t rk = (static_cast<uint64_t>(rev_lane(static_cast<uint32_t>(bk >> 32))) << 32) |
+                      rev_lane(static_cast<uint32_t>(bk));
+  const int32_t rp = static_cast<int32_t>(rev_lane(static_cast<uint32_t>(bp)));
   if (rk < lk[KPL - 1]) {
     lk[KPL - 1] = rk;
     lp[KPL - 1] = rp;
