@@ -156,11 +156,23 @@ def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample, thr
             "sample": f"the whole {len(queries)}-query batch over {threads} threads "
                       f"({dtn:.1f} s wall), same index, reference ovvsIvfPqSearch FORCE_CPU",
             "value_1_thread": len(q1) / dt1,
-            "sample_1_thread": f"first {len(q1)} queries, 1 thread ({dt1:.1f} s)"}
+            "sample_1_thread": f"first {len(q1)} queries, 1 thread ({dt1:.1f} s)",
+            "host_nproc": os.cpu_count(), "host_cpu_model": cpu_model()}
     parity = {"queries": len(queries), "tables": "f32",
               "rows_identical": exact_rows, "distances_bit_identical": bits_equal,
               "rows_differing_beyond_ties": mism, "max_rel_distance_error": dist_err}
     return base, parity
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def _fill_rows(shm_name, shape, cfg, C, a, b):
@@ -317,6 +329,30 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
     qps = nq * args.steps / elapsed
     log(f"{args.steps} timed steps: {elapsed * 1e3 / args.steps:.3f} ms/step, {qps:,.0f} QPS")
 
+    # Smaller batches of the same queries (the config's other batch sizes; reported
+    # beside `value`, which is the whole batch).
+    small = {}
+    for b in (1, 100):
+        if b >= nq:
+            continue
+        for _ in range(3):
+            index.search_device(dq[:b].data_ptr(), b, k, cfg.nprobe, krefine, did[:b].data_ptr(),
+                                dd[:b].data_ptr(), lut_dtype=lut)
+        torch.cuda.synchronize()
+        reps = 50
+        tb = time.perf_counter()
+        for _ in range(reps):
+            index.search_device(dq[:b].data_ptr(), b, k, cfg.nprobe, krefine, did[:b].data_ptr(),
+                                dd[:b].data_ptr(), lut_dtype=lut)
+        torch.cuda.synchronize()
+        small[str(b)] = {"queries_per_s": b * reps / (time.perf_counter() - tb),
+                         "ms_per_batch": (time.perf_counter() - tb) * 1e3 / reps}
+    if small:
+        log("smaller batches: " + ", ".join(f"{b}: {v['queries_per_s']:,.0f} QPS" for b, v in small.items()))
+    # The timed batch's results again (the small batches wrote into the output buffers).
+    step()
+    torch.cuda.synchronize()
+
     dsd = {key: s1[key] - s0[key] for key in s1 if isinstance(s1[key], int)}
     calls = dsd["successful_calls"]
     scan_s = dsd["adc_scan_select_ns"] / calls * 1e-9
@@ -387,6 +423,7 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
         },
         "cpu_baseline": cpu,
         "stage_ms": stage_ms,
+        "smaller_batches": small,
         "qps_host_io": qps_host,
         "recall_at_k": rec,
         "recall_k": k,
