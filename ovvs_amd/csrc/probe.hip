@@ -6,7 +6,8 @@
 // left-to-right sum (reference src/neighbors/indexes.cpp:597-606,
 // src/prim/mixer.cpp:174-199, src/prim/cpu/cpu_prims.cpp:24-106).
 //
-// k_probe_mfma, one workgroup of kWaves wave64s per 16 queries:
+// k_probe_mfma, one workgroup of NW wave64s per 16 queries (8; 16 when the batch
+// gives fewer workgroups than CUs, so that each wave's tile chain is half as long):
 //   pass 1   v_mfma_f32_16x16x32_bf16 tiles of 16 queries x 16 centroids give
 //            approximate scores a(q,c) from split operands: every fp32 value x is
 //            x_hi + x_lo with x_hi = bf16(x), x_lo = bf16(x - x_hi) (round to nearest
@@ -49,10 +50,8 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
+
 constexpr int kRows = 16;                     // queries per workgroup (MFMA M dimension)
-constexpr int kRowsPerWave = kRows / kWaves;  // rows each wave selects and ranks
 constexpr int kMaxChunks = OVVS_PROBE_MAX_GROUPS / 16;
 
 // Launch shape and LDS carve of one probe launch.
@@ -176,9 +175,11 @@ __device__ float candidate_bound(float t, float qn, float cn_max, int dim, int k
   return f;
 }
 
-template <int KS>
-__global__ __launch_bounds__(kThreads) void k_probe_mfma(const OvvsProbeArgs p,
-                                                         const ProbeShape shape) {
+template <int KS, int NW>
+__global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, const ProbeShape shape) {
+  constexpr int kWaves = NW;
+  constexpr int kThreads = 64 * NW;
+  constexpr int kRowsPerWave = kRows / kWaves;  // rows each wave selects and ranks
   extern __shared__ __align__(16) unsigned char smem[];
   const Carve L = carve(smem, shape);
   const int lane = lane_id();
@@ -362,18 +363,26 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
   return sh->lds <= 160 * 1024;
 }
 
-template <int KS>
-hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
+template <int KS, int NW>
+hipError_t launch_probe_nw(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
   if (sh.lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<KS>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<KS, NW>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(sh.lds));
     if (e != hipSuccess) return e;
   }
   const int64_t blocks = (p.nq + kRows - 1) / kRows;
-  hipLaunchKernelGGL(k_probe_mfma<KS>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads),
+  hipLaunchKernelGGL((k_probe_mfma<KS, NW>), dim3(static_cast<uint32_t>(blocks)), dim3(64 * NW),
                      sh.lds, stream, p, sh);
   return hipGetLastError();
+}
+
+// 16 waves per workgroup when the batch gives fewer workgroups than the 256 CUs
+// (small batches: the latency of one workgroup is the launch), else 8.
+template <int KS>
+hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
+  if ((p.nq + kRows - 1) / kRows < 256) return launch_probe_nw<KS, 16>(p, sh, stream);
+  return launch_probe_nw<KS, 8>(p, sh, stream);
 }
 
 }  // namespace
