@@ -230,6 +230,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-small-batches", action="store_true",
+                    help="skip the 1- and 100-query batches (profiling runs)")
     ap.add_argument("--nq", type=int, default=None, help="query batch (default: config's)")
     ap.add_argument("--rows", type=int, default=None,
                     help="base rows (default: config's; a prefix of its stream)")
@@ -332,7 +334,7 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
     # Smaller batches of the same queries (the config's other batch sizes; reported
     # beside `value`, which is the whole batch).
     small = {}
-    for b in (1, 100):
+    for b in (() if args.no_small_batches else (1, 100)):
         if b >= nq:
             continue
         for _ in range(3):
