@@ -7,7 +7,8 @@
 // the first nprobe centroids under the total order (score, centroid index).
 //
 // Kernels:
-//   k_row_norms      one lane per row, sequential sum.
+//   k_row_norms      64 rows per workgroup staged through LDS, one lane per row,
+//                    sequential sum.
 //   k_coarse_scores  64x64 register-tiled VALU GEMM (4x4 outputs per lane, operands
 //                    staged through LDS, 16-deep K slices), sequential per output so
 //                    every score is bit-identical to the reference's.
@@ -27,14 +28,29 @@ constexpr int kTile = 64;    // rows (queries) and columns (centroids) per workg
 constexpr int kSlice = 16;   // K-depth staged per LDS round
 constexpr int kPad = 4;      // LDS row padding (floats) for the transposed tiles
 
+// Norms of 64 rows per workgroup: 64-column slices of the rows are staged in LDS by
+// all 256 threads (coalesced), then thread r sums row r's squares left to right.
+constexpr int kNormRows = 64;
 __global__ __launch_bounds__(256) void k_row_norms(const float* __restrict__ x, int64_t n,
                                                    int dim, float* __restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float* r = x + i * dim;
+  __shared__ float tile[kNormRows][kNormRows + 1];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kNormRows;
+  const int t = static_cast<int>(threadIdx.x);
   float s = 0.f;
-  for (int t = 0; t < dim; ++t) s = s + r[t] * r[t];
-  out[i] = s;
+  for (int d0 = 0; d0 < dim; d0 += kNormRows) {
+    const int dc = dim - d0 < kNormRows ? dim - d0 : kNormRows;
+    __syncthreads();  // the previous slice has been summed
+    for (int e = t; e < kNormRows * kNormRows; e += 256) {
+      const int rr = e / kNormRows, c = e % kNormRows;
+      const int64_t row = r0 + rr;
+      tile[rr][c] = (row < n && c < dc) ? x[row * dim + d0 + c] : 0.f;
+    }
+    __syncthreads();
+    if (t < kNormRows) {
+      for (int c = 0; c < dc; ++c) s = s + tile[t][c] * tile[t][c];
+    }
+  }
+  if (t < kNormRows && r0 + t < n) out[r0 + t] = s;
 }
 
 // Stages the [64 x kSlice] slices of Q (rows q0..) and C (rows c0..) for depth
@@ -280,7 +296,7 @@ extern "C" hipError_t ovvs_hip_row_norms(const float* x, int64_t n, int32_t dim,
                                          hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   if (!x || !out || dim <= 0) return hipErrorInvalidValue;
-  const int64_t blocks = (n + 255) / 256;
+  const int64_t blocks = (n + kNormRows - 1) / kNormRows;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_row_norms, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, x, n,
                      dim, out);

@@ -7,14 +7,16 @@
 // is merged only on success (:1103-1125).
 //
 // Device pipeline per call, all on the Resources stream:
-//   1. query norms                          ovvs_hip_row_norms
-//   2. probe selection, either
-//      a. matrix-core probe with exact       ovvs_hip_probe_mfma, then for the queries
-//         re-score (dim <= 128, enough        it flags ovvs_hip_probe_exact_rows +
-//         centroid groups)                    ovvs_hip_select_topk_flagged
-//      b. exact coarse scores, chunked over  ovvs_hip_coarse_scores +
-//         queries, and row selection         ovvs_hip_select_topk
-//   3. fused LUT + code scan + shortlist    ovvs_hip_scan
+//   1. query norms and probe selection, either
+//      a. matrix-core probe with exact       ovvs_hip_probe_mfma (it also computes the
+//         re-score (dim <= 128, enough        query norms and clears the counters), then
+//         centroid groups)                    for the queries it flags
+//                                             ovvs_hip_probe_exact_rows +
+//                                             ovvs_hip_select_topk_flagged
+//      b. query norms, exact coarse scores   ovvs_hip_row_norms, ovvs_hip_coarse_scores
+//         chunked over queries, row select   + ovvs_hip_select_topk
+//   2. the scan's query order                ovvs_hip_query_order
+//   3. fused LUT + code scan + shortlist    ovvs_hip_scan (+ ovvs_hip_scan_stats)
 //   4. exact re-rank + final select         ovvs_hip_refine
 // There is no host compute path: without a usable GPU the call fails with
 // OVVS_STATUS_DEVICE_UNAVAILABLE.
@@ -182,19 +184,22 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       ovvs::saturating_add(work.h2d_calls, 1);
       ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(qb));
     }
-    SEARCH_HIP(hipMemsetAsync(d_counters, 0, 4 * 8, s));
+    const bool mfma_probe =
+        dv.cmfma.get() != nullptr && ovvs_hip_probe_mfma_supported(dim, ix.nlist, P) != 0;
+    // The matrix-core probe computes the query norms and clears the counters itself.
+    if (!mfma_probe) SEARCH_HIP(hipMemsetAsync(d_counters, 0, 4 * 8, s));
 
     hipEvent_t* ev = res->events;
     SEARCH_HIP(hipEventRecord(ev[0], s));
-    SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
+    if (!mfma_probe) SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
     int64_t chunks = 0;
-    const bool mfma_probe =
-        dv.cmfma.get() != nullptr && ovvs_hip_probe_mfma_supported(dim, ix.nlist, P) != 0;
     if (mfma_probe) {
       // Matrix-core probe with exact re-score; flagged queries take the exact route.
       OvvsProbeArgs pa{};
       pa.queries = d_q;
-      pa.qnorm = d_qn;
+      pa.qnorm = nullptr;
+      pa.qnorm_out = d_qn;
+      pa.zero = d_counters;
       pa.nq = nq;
       pa.dim = dim;
       pa.nlist = ix.nlist;
@@ -293,7 +298,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.invalid = d_counters + 3;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += 6 + 2 * chunks;
+    work.kernel_launches += (mfma_probe ? 5 : 6) + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

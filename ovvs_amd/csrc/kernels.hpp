@@ -74,7 +74,10 @@ hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nro
 
 struct OvvsProbeArgs {
   const float* queries;    // [nq * dim]
-  const float* qnorm;      // [nq], exact row norms
+  const float* qnorm;      // [nq], exact row norms; or nullptr: the probe computes them
+                           // (sequential sums, as ovvs_hip_row_norms) into qnorm_out
+  float* qnorm_out;        // [nq] out when qnorm is nullptr
+  unsigned long long* zero; // [4] set to 0 by the launch (the search's counters), or nullptr
   int64_t nq;
   int32_t dim;
   int32_t nlist;

@@ -67,12 +67,14 @@ struct ProbeShape {
 
 constexpr size_t align16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
 
-// LDS: qs [16][dq] f32 | count [16] i32 | thr [16] f32 | area: gmin [16][16*nch] u32
-// during passes 1-2, then slot [16][cap] u64 (candidate id, later its exact key).
+// LDS: qs [16][dq] f32 | count [16] i32 | thr [16] f32 | qn [16] f32 | area: gmin
+// [16][16*nch] u32 during passes 1-2, then slot [16][cap] u64 (candidate id, later its
+// exact key).
 struct Carve {
   float* qs;
   int32_t* count;
   float* thr;
+  float* qn;
   uint32_t* gmin;
   uint64_t* slot;
 };
@@ -83,7 +85,8 @@ __device__ __forceinline__ Carve carve(unsigned char* base, const ProbeShape& sh
   unsigned char* p = base + align16(static_cast<size_t>(kRows) * sh.dq * 4);
   c.count = reinterpret_cast<int32_t*>(p);
   c.thr = reinterpret_cast<float*>(p + kRows * 4);
-  p += align16(2 * kRows * 4);
+  c.qn = reinterpret_cast<float*>(p + 2 * kRows * 4);
+  p += align16(3 * kRows * 4);
   c.gmin = reinterpret_cast<uint32_t*>(p);
   c.slot = reinterpret_cast<uint64_t*>(p);
   return c;
@@ -194,6 +197,21 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     L.qs[i] = (q < p.nq && t < dim) ? p.queries[q * dim + t] : 0.f;
   }
   if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
+  if (p.zero && blockIdx.x == 0 && threadIdx.x < 4) p.zero[threadIdx.x] = 0;
+  __syncthreads();
+  // Query norms: given, or the sequential sums of squares of the staged rows.
+  if (threadIdx.x < kRows) {
+    const int64_t q = q0 + threadIdx.x;
+    float s = 0.f;
+    if (p.qnorm) {
+      s = q < p.nq ? p.qnorm[q] : 0.f;
+    } else {
+      const float* r = L.qs + threadIdx.x * dq;
+      for (int t = 0; t < dim; ++t) s = s + r[t] * r[t];
+      if (q < p.nq) p.qnorm_out[q] = s;
+    }
+    L.qn[threadIdx.x] = q < p.nq ? s : 0.f;
+  }
   __syncthreads();
 
   bf16x8 ah[KS], al[KS];
@@ -212,7 +230,8 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = q0 + 4 * (lane >> 4) + r;
-    qn[r] = row < p.nq ? p.qnorm[row] : 0.f;
+    qn[r] = L.qn[4 * (lane >> 4) + r];
+    (void)row;
   }
   const int col = lane & 15;
 
@@ -257,7 +276,7 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     }
     if (lane == 0) {
       const int64_t q = q0 + row;
-      const float qnr = q < p.nq ? p.qnorm[q] : 0.f;
+      const float qnr = q < p.nq ? L.qn[row] : 0.f;
       L.thr[row] = candidate_bound(key_to_score(v), qnr, p.cnorm_max, dim, KS);
     }
   }
@@ -310,7 +329,7 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
     const float* qrow = L.qs + row * dq;
     const float dot = (dim & 3) == 0 ? seq_dot_v4(qrow, crow, dim) : seq_dot(qrow, crow, dim);
-    *s = make_key((p.qnorm[q0 + row] + p.cnorm[c]) - 2.f * dot, c);
+    *s = make_key((L.qn[row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();
   for (int f = lane; f < total; f += 64) {
@@ -359,7 +378,7 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
                       (static_cast<size_t>(16 * sh->nch) * 4 > static_cast<size_t>(sh->cap) * 8
                            ? static_cast<size_t>(16 * sh->nch) * 4
                            : static_cast<size_t>(sh->cap) * 8);
-  sh->lds = align16(static_cast<size_t>(kRows) * sh->dq * 4) + align16(2 * kRows * 4) + area;
+  sh->lds = align16(static_cast<size_t>(kRows) * sh->dq * 4) + align16(3 * kRows * 4) + area;
   return sh->lds <= 160 * 1024;
 }
 
@@ -432,7 +451,7 @@ extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t
   const OvvsProbeArgs& p = *args;
   if (p.nq <= 0) return hipSuccess;
   ProbeShape sh;
-  if (!p.queries || !p.qnorm || !p.centroids || !p.cmfma || !p.cnorm || !p.probes ||
+  if (!p.queries || (!p.qnorm && !p.qnorm_out) || !p.centroids || !p.cmfma || !p.cnorm || !p.probes ||
       !p.fallback || p.nq > 0x7fffffff || !probe_shape(p.dim, p.nlist, p.P, &sh))
     return hipErrorInvalidValue;
   switch ((p.dim + 31) / 32) {
