@@ -200,6 +200,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       pa.qnorm = nullptr;
       pa.qnorm_out = d_qn;
       pa.zero = d_counters;
+      pa.list_rank = dv.list_rank.as<int32_t>();
+      pa.key_shift = ovvs_hip_query_key_shift(ix.nlist);
+      pa.order_keys = d_okeys;
       pa.nq = nq;
       pa.dim = dim;
       pa.nlist = ix.nlist;
@@ -236,7 +239,8 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     }
     // The scan's query order (counted in the probe-selection stage, so that the scan
     // stage times the scan kernel alone).
-    SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_okeys, d_order, s));
+    SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_okeys,
+                                    mfma_probe ? 1 : 0, d_order, s));
     SEARCH_HIP(hipEventRecord(ev[2], s));
 
     OvvsScanArgs sa{};
@@ -298,7 +302,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.invalid = d_counters + 3;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += (mfma_probe ? 5 : 6) + 2 * chunks;
+    work.kernel_launches += (mfma_probe ? 4 : 6) + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

@@ -78,6 +78,9 @@ struct OvvsProbeArgs {
                            // (sequential sums, as ovvs_hip_row_norms) into qnorm_out
   float* qnorm_out;        // [nq] out when qnorm is nullptr
   unsigned long long* zero; // [4] set to 0 by the launch (the search's counters), or nullptr
+  const int32_t* list_rank;  // with order_keys: [nlist] spatial rank of every list
+  int32_t key_shift;         // order_keys[q] = list_rank[nearest probe] >> key_shift
+  int32_t* order_keys;       // [nq] out (0 for flagged queries), or nullptr
   int64_t nq;
   int32_t dim;
   int32_t nlist;
@@ -163,9 +166,12 @@ hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
 // order = the queries 0 .. nq-1 sorted by the spatial rank (list_rank, a permutation
 // of the lists) of their nearest probed list (probes[q * P]); the scan hands each
 // XCD one contiguous part of it, so that its L2 serves lists near each other.
-// keys: [nq] workspace.
+// keys: [nq] workspace; with keys_ready it already holds every query's bucket
+// (list_rank[probes[q * P]] >> ovvs_hip_query_key_shift(nlist)).
 hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
-                                int32_t nlist, int32_t* keys, int32_t* order, hipStream_t stream);
+                                int32_t nlist, int32_t* keys, int32_t keys_ready, int32_t* order,
+                                hipStream_t stream);
+int32_t ovvs_hip_query_key_shift(int32_t nlist);
 // counters[i] += sum over the queries of stats[q * 4 + i], i < 4 (the scan's
 // per-query statistics).
 hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq, unsigned long long* counters,

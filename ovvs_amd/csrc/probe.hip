@@ -316,7 +316,10 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     const bool ok = q < p.nq && c >= p.P && c <= cap;
     cnt[rr] = ok ? c : 0;
     pre[rr + 1] = pre[rr] + cnt[rr];
-    if (q < p.nq && lane == 0) p.fallback[q] = ok ? 0 : 1;
+    if (q < p.nq && lane == 0) {
+      p.fallback[q] = ok ? 0 : 1;
+      if (!ok && p.order_keys) p.order_keys[q] = 0;
+    }
   }
   const int total = pre[kRowsPerWave];
   for (int f = lane; f < total; f += 64) {
@@ -342,6 +345,7 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     int rank = 0;
     for (int j = 0; j < cnt[rr]; ++j) rank += keys[j] < key ? 1 : 0;
     if (rank < p.P) p.probes[(q0 + row) * p.P + rank] = static_cast<int32_t>(key & 0xffffffffu);
+    if (rank == 0 && p.order_keys) p.order_keys[q0 + row] = p.list_rank[key & 0xffffffffu] >> p.key_shift;
   }
 }
 

@@ -1390,15 +1390,23 @@ __global__ __launch_bounds__(kOrderThreads) void k_query_order(const int32_t* __
   for (int64_t q = t; q < nq; q += kOrderThreads) order[atomicAdd(&hist[keys[q]], 1)] = static_cast<int32_t>(q);
 }
 
+extern "C" int32_t ovvs_hip_query_key_shift(int32_t nlist) {
+  int32_t shift = 0;
+  while (nlist > 0 && ((nlist - 1) >> shift) >= 4096) ++shift;
+  return shift;
+}
+
 extern "C" hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
-                                           int32_t nlist, int32_t* keys, int32_t* order, hipStream_t stream) {
+                                           int32_t nlist, int32_t* keys, int32_t keys_ready, int32_t* order,
+                                           hipStream_t stream) {
   if (nq <= 0) return hipSuccess;
   if (!probes || !list_rank || !keys || !order || P <= 0 || nlist <= 0 || nq > 0x7fffffff)
     return hipErrorInvalidValue;
-  int shift = 0;
-  while (((nlist - 1) >> shift) >= 4096) ++shift;
-  hipLaunchKernelGGL(k_query_keys, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256), 0, stream, probes, nq,
-                     static_cast<int>(P), list_rank, static_cast<int>(nlist), shift, keys);
+  const int shift = ovvs_hip_query_key_shift(nlist);
+  if (!keys_ready) {
+    hipLaunchKernelGGL(k_query_keys, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256), 0, stream, probes,
+                       nq, static_cast<int>(P), list_rank, static_cast<int>(nlist), shift, keys);
+  }
   hipLaunchKernelGGL(k_query_order, dim3(1), dim3(kOrderThreads), 0, stream, keys, nq, order);
   return hipGetLastError();
 }
