@@ -94,7 +94,9 @@ ovvsStatus ovvsResourcesImpl::ensure_gpu() {
   }
   hipEvent_t ev[kEvents] = {};
   for (int i = 0; i < kEvents; ++i) {
-    if (hipEventCreate(&ev[i]) != hipSuccess) {
+    // Stage timing only (read after the stream is synchronized): no system-scope
+    // fence when recorded, which would write back and invalidate caches mid-search.
+    if (hipEventCreateWithFlags(&ev[i], hipEventDisableSystemFence) != hipSuccess) {
       for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
       (void)hipStreamDestroy(s);
       return OVVS_STATUS_DEVICE_UNAVAILABLE;
