@@ -67,6 +67,8 @@ typedef enum ovvsDType {
 /* Opaque handles (reference include/ovvs/ovvs.h:77,80). */
 typedef struct ovvsResourcesImpl* ovvsResources_t;
 typedef struct ovvsIvfPqIndexImpl* ovvsIvfPqIndex_t;
+/* reference include/ovvs/ovvs.h:77 */
+typedef struct ovvsScannIndexImpl* ovvsScannIndex_t;
 
 #define OVVS_IVF_PQ_SEARCH_STATS_ABI_V1 1u
 
@@ -168,6 +170,31 @@ OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t 
                                           int32_t nprobe, int32_t krefine,
                                           const uint8_t* bitset, ovvsDType lut_dtype,
                                           int64_t* neighbors, float* distances);
+
+/* ScaNN-style index: IVF-PQ trained on column-scaled rows, re-ranked in the
+ * original space (reference include/ovvs/ovvs.h:393-399,
+ * src/neighbors/graphs.cpp:3286-3385).
+ *
+ * Build: aniso[d] = sqrt(var_d + 1e-6) per column (population variance from
+ * left-to-right fp32 sums), computed on the GPU; the index keeps the rows and an
+ * IVF-PQ index built by ovvsIvfPqBuild (8-bit codes) on the rows scaled by
+ * aniso. On failure the build returns the inner build's status and leaves
+ * *index unchanged, as the reference does.
+ *
+ * Search: krefine := max(krefine, (int32)k); the queries scaled by aniso are
+ * searched with ovvsIvfPqSearch semantics for krefine results (k = krefine),
+ * which counts in the IVF-PQ telemetry as one search; the returned ids are
+ * re-ranked by the index metric on the original rows and queries, the first
+ * min(k, candidates) by (distance, result rank) are written, inner-product
+ * distances as +ip, the rest padded with (-1, +inf). k <= 0 writes nothing and
+ * succeeds when the inner search does. Every step runs on the GPU. */
+OVVS_API ovvsStatus ovvsScannBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                   int64_t dim, ovvsMetric metric, int32_t nlist, int32_t pq_m,
+                                   ovvsScannIndex_t* index);
+OVVS_API ovvsStatus ovvsScannSearch(ovvsResources_t res, ovvsScannIndex_t index,
+                                    const float* queries, int64_t nq, int64_t k, int32_t nprobe,
+                                    int32_t krefine, int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsScannDestroy(ovvsScannIndex_t index);
 
 /* Allow-list to an LSB-first bitset of (n+7)/8 bytes; ids outside [0,n) are
  * ignored (reference include/ovvs/ovvs.h:406, src/rt/resources.cpp:218-229). */

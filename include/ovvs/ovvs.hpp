@@ -82,4 +82,27 @@ class IvfPqIndex {
   ovvsIvfPqIndex_t ix_ = nullptr;
 };
 
+// reference include/ovvs/ovvs.hpp:221-241
+class ScannIndex {
+ public:
+  ScannIndex(Resources& res, const float* dataset, int64_t n, int64_t dim, ovvsMetric metric,
+             int32_t nlist, int32_t pq_m)
+      : res_(&res) {
+    check(ovvsScannBuild(res.get(), dataset, n, dim, metric, nlist, pq_m, &ix_));
+  }
+  ~ScannIndex() {
+    if (ix_) ovvsScannDestroy(ix_);
+  }
+  ScannIndex(const ScannIndex&) = delete;
+  ScannIndex& operator=(const ScannIndex&) = delete;
+  void search(const float* queries, int64_t nq, int64_t k, int32_t nprobe, int32_t krefine,
+              int64_t* neighbors, float* distances) {
+    check(ovvsScannSearch(res_->get(), ix_, queries, nq, k, nprobe, krefine, neighbors, distances));
+  }
+
+ private:
+  Resources* res_ = nullptr;
+  ovvsScannIndex_t ix_ = nullptr;
+};
+
 }  // namespace ovvs

@@ -18,7 +18,9 @@
  *   final            first min(k, kr) by (v, shortlist rank), IP sign flip,
  *                    (-1, +inf) padding                               indexes.cpp:1080-1096
  * plus the declared binary16-LUT extension (no reference counterpart):
- * T16 = f16_rne(T), accumulated in fp32.
+ * T16 = f16_rne(T), accumulated in fp32, and the ScaNN-style index around the
+ * search (graphs.cpp:3286-3374): column factors sqrt(var + 1e-6) of the build,
+ * scaled queries, re-rank of the returned ids on the original rows.
  *
  * Pinning: every function here is checked in tests/test_oracle.py against the
  * real reference compiled from /root/reference into oracle/_ref (bit-identical
@@ -26,7 +28,10 @@
  * known-answer cases (legacy IPQ1 blob, equal-score ties, cross-list ties,
  * filters), and against closed forms (nprobe = nlist with krefine = n equals
  * exact brute force). oracle_f32_to_f16 is pinned against numpy's float16
- * conversion (an independent IEEE round-to-nearest-even implementation). */
+ * conversion (an independent IEEE round-to-nearest-even implementation). The
+ * ScaNN functions are pinned against the reference's own ScaNN answers
+ * (tests/golden/scann_cases.*, and oracle/_ref live), closed-form column
+ * statistics, and brute force at full probe and refine. */
 
 #include <math.h>
 #include <stdint.h>
@@ -405,4 +410,74 @@ int oracle_brute_force(const float* dataset, int64_t n, int64_t dim, int32_t met
   free(idx);
   free(val);
   return 0;
+}
+
+/* ---- ScaNN-style index (graphs.cpp:3286-3374) ---- */
+
+/* Column factors of the build (graphs.cpp:3291-3301): m = (sum_i x[i][d]) / n,
+ * v = sum_i (x[i][d] - m)^2, aniso[d] = sqrt(v / max(n, 1) + 1e-6), every sum
+ * left to right in fp32. */
+void oracle_scann_aniso(const float* x, int64_t n, int64_t dim, float* aniso) {
+  for (int64_t d = 0; d < dim; ++d) {
+    float m = 0.f;
+    for (int64_t i = 0; i < n; ++i) m += x[i * dim + d];
+    m /= (float)n;
+    float v = 0.f;
+    for (int64_t i = 0; i < n; ++i) {
+      const float t = x[i * dim + d] - m;
+      v += t * t;
+    }
+    aniso[d] = sqrtf(v / (float)(n > 1 ? n : 1) + 1e-6f);
+  }
+}
+
+/* Search (graphs.cpp:3316-3374): R = max(krefine, k); IVF-PQ search of the
+ * queries scaled column-wise by aniso for R results (k = R) on `ix` (the index
+ * built on the scaled rows); then per query the returned ids in [0, n), in result
+ * order, re-ranked by the index metric on the original rows and queries, the first
+ * min(k, count) by (distance, position) written (inner product as +ip) and the
+ * rest padded with (-1, +inf). Returns 0, or -1 when the inner search fails. */
+int oracle_scann_search(const oracle_index* ix, const float* rows, int64_t n, const float* aniso,
+                        const float* queries, int64_t nq, int64_t k, int32_t nprobe,
+                        int32_t krefine, int64_t* neighbors, float* distances) {
+  const int64_t dim = ix->dim;
+  const int32_t R = krefine < (int32_t)k ? (int32_t)k : krefine;
+  if (nq <= 0 || R <= 0) return -1;
+  float* qs = (float*)malloc((size_t)nq * (size_t)dim * sizeof(float));
+  int64_t* cand = (int64_t*)malloc((size_t)nq * (size_t)R * sizeof(int64_t));
+  float* cd = (float*)malloc((size_t)nq * (size_t)R * sizeof(float));
+  int64_t* ids = (int64_t*)malloc((size_t)R * sizeof(int64_t));
+  float* v = (float*)malloc((size_t)R * sizeof(float));
+  int64_t* idx = (int64_t*)malloc((size_t)R * sizeof(int64_t));
+  float* val = (float*)malloc((size_t)R * sizeof(float));
+  int rc = -1;
+  if (!qs || !cand || !cd || !ids || !v || !idx || !val) goto done;
+  for (int64_t i = 0; i < nq; ++i)
+    for (int64_t d = 0; d < dim; ++d) qs[i * dim + d] = queries[i * dim + d] * aniso[d];
+  if (oracle_ivfpq_search(ix, qs, nq, R, nprobe, R, NULL, 0, cand, cd) != 0) goto done;
+  for (int64_t q = 0; q < nq; ++q) {
+    int64_t m = 0;
+    for (int32_t t = 0; t < R; ++t) {
+      const int64_t id = cand[q * R + t];
+      if (id >= 0 && id < n) ids[m++] = id;
+    }
+    for (int64_t i = 0; i < m; ++i)
+      v[i] = oracle_refine_distance(ix->metric, queries + q * dim, rows + ids[i] * dim, dim);
+    const int64_t kk = oracle_topk(v, m, k, idx, val);
+    if (kk < 0) goto done;
+    for (int64_t t = 0; t < k; ++t) {
+      neighbors[q * k + t] = t < kk ? ids[idx[t]] : -1;
+      distances[q * k + t] = t < kk ? (ix->metric == OR_IP ? -val[t] : val[t]) : INFINITY;
+    }
+  }
+  rc = 0;
+done:
+  free(qs);
+  free(cand);
+  free(cd);
+  free(ids);
+  free(v);
+  free(idx);
+  free(val);
+  return rc;
 }

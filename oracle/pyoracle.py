@@ -187,6 +187,27 @@ class Oracle:
                                        ctypes.byref(total))
         return pos[:kr], sc[:kr], int(total.value)
 
+    def scann_search(self, rows, aniso, queries, k, nprobe, krefine):
+        """ScaNN-style search (reference graphs.cpp:3316-3374) with this index as the
+        IVF-PQ over the scaled rows, `rows` the original rows and `aniso` the column
+        factors (oracle_scann_aniso)."""
+        L = self.lib
+        L.oracle_scann_search.restype = c_int32
+        L.oracle_scann_search.argtypes = [POINTER(_OracleIndex), POINTER(c_float), c_int64,
+                                          POINTER(c_float), POINTER(c_float), c_int64, c_int64,
+                                          c_int32, c_int32, POINTER(c_int64), POINTER(c_float)]
+        x = np.ascontiguousarray(rows, dtype=np.float32)
+        a = np.ascontiguousarray(aniso, dtype=np.float32)
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.ix.dim)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), dtype=np.int64)
+        dists = np.empty((nq, k), dtype=np.float32)
+        rc = L.oracle_scann_search(ctypes.byref(self.s), _f32p(x), x.shape[0], _f32p(a), _f32p(q),
+                                   nq, k, nprobe, krefine, _i64p(ids), _f32p(dists))
+        if rc != 0:
+            raise MemoryError("oracle ScaNN search failed")
+        return ids, dists
+
     def lut(self, query, list_id, lut_f16=False):
         q = np.ascontiguousarray(query, dtype=np.float32).reshape(self.ix.dim)
         t = np.empty((self.ix.pq_m, self.ix.pq_ks), dtype=np.float32)
@@ -211,6 +232,17 @@ def oracle_lib():
     lib.oracle_refine_distance.restype = c_float
     lib.oracle_refine_distance.argtypes = [c_int32, POINTER(c_float), POINTER(c_float), c_int64]
     return lib
+
+
+def scann_aniso(rows):
+    """Column factors of the ScaNN-style build (oracle_scann_aniso)."""
+    x = np.ascontiguousarray(rows, dtype=np.float32)
+    lib = ctypes.CDLL(str(ORACLE_SO))
+    lib.oracle_scann_aniso.restype = None
+    lib.oracle_scann_aniso.argtypes = [POINTER(c_float), c_int64, c_int64, POINTER(c_float)]
+    out = np.empty(x.shape[1], dtype=np.float32)
+    lib.oracle_scann_aniso(_f32p(x), x.shape[0], x.shape[1], _f32p(out))
+    return out
 
 
 def brute_force(dataset, queries, k, metric=0):
@@ -244,6 +276,11 @@ class Reference:
             "ovvsIvfPqDeserialize": [V, c_char_p, POINTER(V)],
             "ovvsIvfPqExtend": [V, V, POINTER(c_float), c_int64],
             "ovvsIvfPqDestroy": [V],
+            "ovvsScannBuild": [V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32, c_int32,
+                               POINTER(V)],
+            "ovvsScannSearch": [V, V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
+                                POINTER(c_int64), POINTER(c_float)],
+            "ovvsScannDestroy": [V],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -327,3 +364,23 @@ class Reference:
     def destroy(self, h):
         if h:
             self.lib.ovvsIvfPqDestroy(h)
+
+    def scann_build(self, data, metric, nlist, pq_m):
+        x = np.ascontiguousarray(data, dtype=np.float32)
+        h = c_void_p()
+        rc = self.lib.ovvsScannBuild(self.res, _f32p(x), x.shape[0], x.shape[1], metric, nlist,
+                                     pq_m, ctypes.byref(h))
+        return rc, h
+
+    def scann_search(self, h, queries, k, nprobe, krefine):
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        nq = q.shape[0]
+        ids = np.full((nq, max(k, 0)), -9, dtype=np.int64)
+        d = np.full((nq, max(k, 0)), -9.0, dtype=np.float32)
+        rc = self.lib.ovvsScannSearch(self.res, h, _f32p(q), nq, k, nprobe, krefine, _i64p(ids),
+                                      _f32p(d))
+        return rc, ids, d
+
+    def scann_destroy(self, h):
+        if h:
+            self.lib.ovvsScannDestroy(h)

@@ -28,6 +28,7 @@ __all__ = [
     "OvvsError",
     "Resources",
     "IvfPqIndex",
+    "ScannIndex",
     "neighbors",
     "bitset_from_allow_list",
     "version",
@@ -121,6 +122,11 @@ _SIGS = {
     "ovvsIvfPqExtend": (c_int32, [_V, _V, POINTER(c_float), c_int64]),
     "ovvsIvfPqDestroy": (c_int32, [_V]),
     "ovvsBitsetFromAllowList": (c_int32, [c_int64, POINTER(c_int64), c_int64, POINTER(c_uint8)]),
+    "ovvsScannBuild": (c_int32, [_V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32, c_int32,
+                                 POINTER(_V)]),
+    "ovvsScannSearch": (c_int32, [_V, _V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
+                                  POINTER(c_int64), POINTER(c_float)]),
+    "ovvsScannDestroy": (c_int32, [_V]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -304,7 +310,57 @@ class IvfPqIndex:
         return x
 
 
+class ScannIndex:
+    """Handle of a ScaNN-style index (reference python/ovvs/__init__.py:1189-1243)."""
+
+    def __init__(self, res: Resources, handle: c_void_p, dim: int, own_res: bool, n: int = 0):
+        self._res = res
+        self._h = handle
+        self.dim = int(dim)
+        self.n = int(n)
+        self._own = own_res
+
+    def close(self):
+        if self._h:
+            _lib.ovvsScannDestroy(self._h)
+            self._h = None
+        if self._own and self._res is not None:
+            self._res.close()
+            self._res = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def resources(self) -> Resources:
+        return self._res
+
+    def search(self, queries, k=10, nprobe=8, krefine=32):
+        q = _f32_matrix(queries, self.dim)
+        nq = q.shape[0]
+        ids = np.empty((nq, int(k)), dtype=np.int64)
+        dists = np.empty((nq, int(k)), dtype=np.float32)
+        rc = _lib.ovvsScannSearch(self._res._h, self._h, q.ctypes.data_as(POINTER(c_float)),
+                                  c_int64(nq), c_int64(k), c_int32(nprobe), c_int32(krefine),
+                                  ids.ctypes.data_as(POINTER(c_int64)),
+                                  dists.ctypes.data_as(POINTER(c_float)))
+        _check_status(rc, "ScaNN search")
+        return ids, dists
+
+
 class neighbors:
+    class scann:
+        @staticmethod
+        def build(dataset, dim=None, metric=0, nlist=8, pq_m=8, resources=None):
+            res = resources or Resources()
+            x = _f32_matrix(dataset, dim)
+            h = c_void_p()
+            rc = _lib.ovvsScannBuild(res._h, x.ctypes.data_as(POINTER(c_float)),
+                                     c_int64(x.shape[0]), c_int64(x.shape[1]), c_int32(metric),
+                                     c_int32(nlist), c_int32(pq_m), ctypes.byref(h))
+            _check_status(rc, "ScaNN build")
+            return ScannIndex(res, h, x.shape[1], own_res=resources is None, n=x.shape[0])
+
     class ivf_pq:
         @staticmethod
         def build(dataset, dim=None, metric=0, nlist=8, pq_m=8, pq_nbits=8, resources=None):

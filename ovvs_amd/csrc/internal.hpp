@@ -152,13 +152,19 @@ struct ovvsResourcesImpl {
   ovvs::DeviceBuffer workspace;
   void* pinned = nullptr;
   size_t pinned_bytes = 0;
+  // Entry points built on other entry points (the ScaNN search around the
+  // IVF-PQ search) hold outer_mutex for the whole call and keep their own
+  // buffers in outer_workspace, which the inner call does not touch.
+  std::mutex outer_mutex;
+  ovvs::DeviceBuffer outer_workspace;
 
   ~ovvsResourcesImpl();
   // Opens the current HIP device, its stream and events. Returns
   // DEVICE_UNAVAILABLE without a GPU or when the policy forces another device.
   ovvsStatus ensure_gpu();
-  // Grows the device workspace to at least `bytes`.
+  // Grows the device workspace (the outer workspace) to at least `bytes`.
   ovvsStatus reserve_workspace(size_t bytes, ovvs::GpuWork& work);
+  ovvsStatus reserve_outer_workspace(size_t bytes, ovvs::GpuWork& work);
   // Grows the pinned host staging buffer to at least `bytes`.
   ovvsStatus reserve_pinned(size_t bytes);
 };
@@ -187,6 +193,11 @@ struct ovvsIvfPqIndexImpl {
 };
 
 namespace ovvs {
+// Argument checks of ovvsIvfPqBuild after the null checks, in its order:
+// INVALID_ARGUMENT for non-positive sizes or an unknown metric, SHAPE_MISMATCH
+// when pq_m does not divide dim or the sizes overflow.
+ovvsStatus ivf_pq_build_arg_status(int64_t n, int64_t dim, ovvsMetric metric, int32_t nlist,
+                                   int32_t pq_m);
 // Checks the invariants of a list layout: every id in [0, n) exactly once,
 // listed under its own assignment, codes < ks (reference indexes.cpp:59-114).
 bool lists_valid(const ovvsIvfPqIndexImpl& ix);

@@ -238,6 +238,20 @@ bool fits_size(uint64_t a, uint64_t b) {
 
 namespace ovvs {
 
+ovvsStatus ivf_pq_build_arg_status(int64_t n, int64_t dim, ovvsMetric metric, int32_t nlist,
+                                   int32_t pq_m) {
+  if (n <= 0 || dim <= 0 || nlist <= 0 || pq_m <= 0) return OVVS_STATUS_INVALID_ARGUMENT;
+  if (metric < OVVS_METRIC_L2_EXPANDED || metric > OVVS_METRIC_LP_UNEXPANDED) {
+    return OVVS_STATUS_INVALID_ARGUMENT;
+  }
+  if (dim % pq_m != 0) return OVVS_STATUS_SHAPE_MISMATCH;
+  if (n > std::numeric_limits<int32_t>::max() || dim > std::numeric_limits<int32_t>::max() ||
+      !fits_size(static_cast<uint64_t>(n), static_cast<uint64_t>(dim) * 4)) {
+    return OVVS_STATUS_SHAPE_MISMATCH;
+  }
+  return OVVS_STATUS_SUCCESS;
+}
+
 bool lists_valid(const ovvsIvfPqIndexImpl& ix) {
   if (ix.n <= 0 || ix.nlist <= 0 || ix.pq_m <= 0 || ix.pq_ks <= 0 || ix.pq_ks > 256 ||
       ix.lists.size() != static_cast<size_t>(ix.nlist) ||
@@ -354,17 +368,8 @@ OVVS_API ovvsStatus ovvsIvfPqBuild(ovvsResources_t res, const float* dataset, in
                                    int64_t dim, ovvsMetric metric, int32_t nlist, int32_t pq_m,
                                    int32_t pq_nbits, ovvsIvfPqIndex_t* index) {
   if (index) *index = nullptr;
-  if (!res || !dataset || !index || n <= 0 || dim <= 0 || nlist <= 0 || pq_m <= 0) {
-    return OVVS_STATUS_INVALID_ARGUMENT;
-  }
-  if (metric < OVVS_METRIC_L2_EXPANDED || metric > OVVS_METRIC_LP_UNEXPANDED) {
-    return OVVS_STATUS_INVALID_ARGUMENT;
-  }
-  if (dim % pq_m != 0) return OVVS_STATUS_SHAPE_MISMATCH;
-  if (n > std::numeric_limits<int32_t>::max() || dim > std::numeric_limits<int32_t>::max() ||
-      !fits_size(static_cast<uint64_t>(n), static_cast<uint64_t>(dim) * 4)) {
-    return OVVS_STATUS_SHAPE_MISMATCH;
-  }
+  if (!res || !dataset || !index) return OVVS_STATUS_INVALID_ARGUMENT;
+  OVVS_TRY(ovvs::ivf_pq_build_arg_status(n, dim, metric, nlist, pq_m));
   nlist = static_cast<int32_t>(std::min<int64_t>(nlist, n));
   const int32_t ks = 1 << std::min(std::max(pq_nbits, 4), 8);
   try {

@@ -206,6 +206,19 @@ struct OvvsRefineArgs {
 // inner-product distances are returned as +ip (reference indexes.cpp:1067-1096).
 hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream);
 
+// ScaNN-style index (reference src/neighbors/graphs.cpp:3286-3374).
+// aniso[d] = sqrt(var_d / max(n, 1) + 1e-6) from left-to-right fp32 column sums
+// (mean = sum / n, then var_d = sum of (x - mean)^2); one thread per column.
+hipError_t ovvs_hip_column_aniso(const float* x, int64_t n, int32_t dim, float* aniso,
+                                 hipStream_t stream);
+// out[i*dim+d] = x[i*dim+d] * s[d]
+hipError_t ovvs_hip_scale_columns(const float* x, int64_t rows, int32_t dim, const float* s,
+                                  float* out, hipStream_t stream);
+// Re-rank candidates from IVF-PQ results ids [nq * R]: pos[q*R+j] = q*R + t for the
+// j-th result t whose id lies in [0, n), count[q] = j. nq * R < 2^31.
+hipError_t ovvs_hip_ids_shortlist(const int64_t* ids, int64_t nq, int32_t R, int64_t n,
+                                  int32_t* pos, int32_t* count, hipStream_t stream);
+
 // ---- index build helpers (reference indexes.cpp:459-536, mixer.cpp:866-921) ----
 
 // out[i*dsub+u] = x[i*dim + m*dsub + u]

@@ -74,6 +74,7 @@ ovvsResourcesImpl::~ovvsResourcesImpl() {
       if (e) (void)hipEventDestroy(e);
     }
     workspace.reset();
+    outer_workspace.reset();
     if (pinned) (void)hipHostFree(pinned);
     (void)hipStreamDestroy(stream);
   }
@@ -109,16 +110,19 @@ ovvsStatus ovvsResourcesImpl::ensure_gpu() {
   return OVVS_STATUS_SUCCESS;
 }
 
-ovvsStatus ovvsResourcesImpl::reserve_workspace(size_t bytes, ovvs::GpuWork& work) {
-  if (workspace.size() >= bytes) return OVVS_STATUS_SUCCESS;
+namespace {
+
+ovvsStatus grow_buffer(ovvs::DeviceBuffer& buf, size_t bytes, hipStream_t stream,
+                       ovvs::GpuWork& work) {
+  if (buf.size() >= bytes) return OVVS_STATUS_SUCCESS;
   (void)hipStreamSynchronize(stream);
   // Grow geometrically so repeated calls with slowly growing batches settle.
-  size_t want = workspace.size() * 2;
+  size_t want = buf.size() * 2;
   if (want < bytes) want = bytes;
-  hipError_t e = workspace.allocate(want);
+  hipError_t e = buf.allocate(want);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    e = workspace.allocate(bytes);
+    e = buf.allocate(bytes);
     want = bytes;
   }
   if (e != hipSuccess) {
@@ -128,6 +132,16 @@ ovvsStatus ovvsResourcesImpl::reserve_workspace(size_t bytes, ovvs::GpuWork& wor
   ovvs::saturating_add(work.allocation_calls, 1);
   ovvs::saturating_add(work.allocation_bytes, static_cast<int64_t>(want));
   return OVVS_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+ovvsStatus ovvsResourcesImpl::reserve_workspace(size_t bytes, ovvs::GpuWork& work) {
+  return grow_buffer(workspace, bytes, stream, work);
+}
+
+ovvsStatus ovvsResourcesImpl::reserve_outer_workspace(size_t bytes, ovvs::GpuWork& work) {
+  return grow_buffer(outer_workspace, bytes, stream, work);
 }
 
 ovvsStatus ovvsResourcesImpl::reserve_pinned(size_t bytes) {

@@ -161,7 +161,6 @@ __device__ __forceinline__ void bitonic_merge_asc(uint64_t (&lk)[KPL], int32_t (
 template <int KPL>
 __device__ __forceinline__ void merge64(uint64_t (&lk)[KPL], int32_t (&lp)[KPL], uint64_t bk,
                                         int32_t bp) {
-  const int lane = lane_id();
   const uint64_t rk = (static_cast<uint64_t>(rev_lane(static_cast<uint32_t>(bk >> 32))) << 32) |
                       rev_lane(static_cast<uint32_t>(bk));
   const int32_t rp = static_cast<int32_t>(rev_lane(static_cast<uint32_t>(bp)));

@@ -261,3 +261,46 @@ def test_build_and_extend_argument_checks(ovvs):
     assert lib.ovvsIvfPqExtend(res._h, ix, xp, 0) == 2
     assert lib.ovvsIvfPqExtend(None, ix, xp, 1) == 2
     lib.ovvsIvfPqDestroy(ix)
+
+
+def test_scann_argument_checks(ovvs):
+    """ScaNN entry points (reference src/neighbors/graphs.cpp:3286-3385): null
+    pointers are INVALID_ARGUMENT, a failed build leaves *index as it was, the inner
+    IVF-PQ build's argument checks apply, and destroying NULL succeeds."""
+    lib = ovvs._lib
+    res = ovvs.Resources()
+    x = np.zeros((8, 4), dtype=np.float32)
+    xp = x.ctypes.data_as(POINTER(c_float))
+    h = c_void_p(5)
+    assert lib.ovvsScannBuild(None, xp, 8, 4, 0, 2, 2, byref(h)) == 2
+    assert lib.ovvsScannBuild(res._h, None, 8, 4, 0, 2, 2, byref(h)) == 2
+    assert lib.ovvsScannBuild(res._h, xp, 8, 4, 0, 2, 2, None) == 2
+    assert lib.ovvsScannBuild(res._h, xp, 0, 4, 0, 2, 2, byref(h)) == 2
+    assert lib.ovvsScannBuild(res._h, xp, 8, 4, 6, 2, 2, byref(h)) == 2   # bad metric
+    assert lib.ovvsScannBuild(res._h, xp, 8, 4, 0, 0, 2, byref(h)) == 2   # nlist <= 0
+    assert lib.ovvsScannBuild(res._h, xp, 8, 4, 0, 2, 3, byref(h)) == 6   # dim % pq_m
+    assert h.value == 5
+    q = np.zeros((1, 4), dtype=np.float32)
+    qp = q.ctypes.data_as(POINTER(c_float))
+    ids = np.full(4, 7, dtype=np.int64)
+    d = np.full(4, -3.0, dtype=np.float32)
+    ip, dp = ids.ctypes.data_as(POINTER(c_int64)), d.ctypes.data_as(POINTER(c_float))
+    fake = c_void_p(1)  # never dereferenced: the null checks come first
+    assert lib.ovvsScannSearch(None, fake, qp, 1, 4, 1, 4, ip, dp) == 2
+    assert lib.ovvsScannSearch(res._h, None, qp, 1, 4, 1, 4, ip, dp) == 2
+    assert lib.ovvsScannSearch(res._h, fake, None, 1, 4, 1, 4, ip, dp) == 2
+    assert lib.ovvsScannSearch(res._h, fake, qp, 1, 4, 1, 4, None, dp) == 2
+    assert lib.ovvsScannSearch(res._h, fake, qp, 1, 4, 1, 4, ip, None) == 2
+    assert np.all(ids == 7) and np.all(d == -3.0)
+    assert lib.ovvsScannDestroy(None) == 0
+
+
+def test_scann_build_without_gpu_is_device_unavailable(ovvs):
+    res = ovvs.Resources()
+    if res.gpu_available():
+        pytest.skip("a GPU is present")
+    x = np.zeros((16, 4), dtype=np.float32)
+    h = c_void_p(5)
+    rc = ovvs._lib.ovvsScannBuild(res._h, x.ctypes.data_as(POINTER(c_float)), 16, 4, 0, 2, 2,
+                                  byref(h))
+    assert rc == 7 and h.value == 5

@@ -9,7 +9,10 @@ tie order, a sign error) fails one of them:
   * the reference tests' known answers: legacy IPQ1 query, equal-score ties,
     cross-list ties, filters;
   * the closed form nprobe = nlist, krefine >= n, which is exact brute force;
-  * binary16 conversion against numpy's independent IEEE implementation.
+  * binary16 conversion against numpy's independent IEEE implementation;
+  * the ScaNN-style search: the reference's own ScaNN answers
+    (tests/golden/scann_cases.*, and oracle/_ref live), closed-form column
+    statistics, and brute force at full probe and refine.
 """
 
 from __future__ import annotations
@@ -18,7 +21,8 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN, case_data, write_case_ipq1
-from oracle.pyoracle import REF_SO, Oracle, Reference, brute_force, oracle_lib, read_ipq1
+from oracle.pyoracle import (REF_SO, Oracle, Reference, brute_force, oracle_lib, read_ipq1,
+                             scann_aniso)
 from ovvs_amd.synth import lcg_data
 
 
@@ -195,3 +199,117 @@ def test_ipq1_writer_round_trips_reference_files(ref_cases, tmp_path):
     p = tmp_path / "legacy.ipq1"
     p.write_bytes(legacy)
     assert read_ipq1(p).to_bytes() == legacy
+
+
+# ---- ScaNN-style index (reference src/neighbors/graphs.cpp:3286-3374) ----
+
+def scann_cases():
+    import json
+
+    manifest = json.loads((GOLDEN / "scann_cases.json").read_text())
+    arrays = np.load(GOLDEN / "scann_cases.npz")
+    return manifest, {k: arrays[k] for k in arrays.files}
+
+
+def _scann_inputs(case):
+    return lcg_data(*case["data_lcg"]), lcg_data(*case["queries_lcg"])
+
+
+def _inner_oracle(case, arrays, tmp_path):
+    p = tmp_path / f"{case['name']}_inner.ipq1"
+    p.write_bytes(arrays[f"{case['name']}/inner_ipq1"].tobytes())
+    return Oracle(read_ipq1(p))
+
+
+def test_scann_aniso_closed_forms():
+    """Columns whose mean and population variance are exact in fp32: a constant
+    column (variance 0, so the factor is sqrt(1e-6)), two- and four-valued columns,
+    one far from zero (the mean must be subtracted) and one centred at zero. A
+    sample variance (n - 1), a dropped 1e-6 or a missing centring fails."""
+    n = 8
+    x = np.zeros((n, 5), np.float32)
+    x[:, 0] = 3.0
+    x[:, 1] = np.tile([0.0, 2.0], n // 2)
+    x[:, 2] = np.tile([1.0, 2.0, 3.0, 4.0], n // 4)
+    x[:, 3] = 1000.0 + np.tile([0.0, 1.0], n // 2)
+    x[:, 4] = np.tile([-2.0, 0.0, 0.0, 2.0], n // 4)
+    var = np.array([0.0, 1.0, 1.25, 0.25, 2.0], np.float32)
+    want = np.sqrt(var + np.float32(1e-6)).astype(np.float32)
+    assert np.array_equal(_bits(scann_aniso(x)), _bits(want))
+    # One row: variance 0 over max(n, 1) = 1.
+    assert np.array_equal(_bits(scann_aniso(x[:1])), _bits(np.full(5, want[0], np.float32)))
+
+
+def test_scann_aniso_tracks_float64_statistics():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3000, 12)) * np.linspace(0.1, 8.0, 12) + 3.0).astype(np.float32)
+    a = scann_aniso(x)
+    want = np.sqrt(x.astype(np.float64).var(axis=0) + 1e-6)
+    assert np.allclose(a, want, rtol=2e-5, atol=0)
+
+
+def test_scann_oracle_reproduces_reference_answers(tmp_path):
+    """The oracle's ScaNN search over the fixture's inner index (the reference's
+    IVF-PQ build of the rows scaled by the oracle's factors) gives the reference
+    ScaNN's own answers bit for bit, so both the factors and the re-rank agree."""
+    manifest, arrays = scann_cases()
+    checked = 0
+    for case in manifest:
+        data, q = _scann_inputs(case)
+        aniso = scann_aniso(data)
+        orc = _inner_oracle(case, arrays, tmp_path)
+        assert np.array_equal(_bits(orc.ix.dataset), _bits(data * aniso[None, :])), case["name"]
+        for j, s in enumerate(case["searches"]):
+            key = f"{case['name']}/s{j}"
+            assert s["rc"] == 0, key
+            if s["k"] == 0:
+                continue
+            ids, d = orc.scann_search(data, aniso, q, s["k"], s["nprobe"], s["krefine"])
+            assert np.array_equal(ids, arrays[f"{key}/ids"]), key
+            assert np.array_equal(_bits(d), _bits(arrays[f"{key}/dists"])), key
+            checked += 1
+    assert checked >= 10
+
+
+def test_scann_full_probe_full_refine_is_brute_force(tmp_path):
+    """The reference test's closed form (tests/test_neighbors.cpp:2958-2967): every
+    list probed and krefine = n make the search exact nearest neighbours of the
+    original rows."""
+    manifest, arrays = scann_cases()
+    case = next(c for c in manifest if c["name"] == "ref_b")
+    data, q = _scann_inputs(case)
+    orc = _inner_oracle(case, arrays, tmp_path)
+    ids, d = orc.scann_search(data, scann_aniso(data), q, 4, case["nlist"], data.shape[0])
+    bids, bd = brute_force(data, q, 4, 0)
+    assert np.array_equal(ids, bids) and np.array_equal(_bits(d), _bits(bd))
+
+
+@pytest.mark.skipif(not REF_SO.exists(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("seed", [1, 2])
+def test_scann_oracle_matches_live_reference(seed, tmp_path):
+    rng = np.random.default_rng(100 + seed)
+    ref = Reference()
+    dim = int(rng.choice([8, 16, 24]))
+    pq_m = int(rng.choice([d for d in (2, 4, 8) if dim % d == 0]))
+    n = int(rng.integers(300, 1200))
+    nlist = int(rng.integers(2, 24))
+    metric = int(rng.choice([0, 1, 2, 3, 5]))
+    data = (rng.standard_normal((n, dim)) * rng.uniform(0.2, 5.0, dim)).astype(np.float32)
+    q = (rng.standard_normal((11, dim)) * rng.uniform(0.2, 5.0, dim)).astype(np.float32)
+    rc, h = ref.scann_build(data, metric, nlist, pq_m)
+    assert rc == 0
+    aniso = scann_aniso(data)
+    rc, inner = ref.build(data * aniso[None, :], metric, nlist, pq_m, 8)
+    assert rc == 0
+    path = tmp_path / "inner.ipq1"
+    assert ref.save(inner, path) == 0
+    orc = Oracle(read_ipq1(path))
+    for k, nprobe, krefine in [(10, 3, 30), (6, nlist, 4), (12, 1, 12)]:
+        rc, rids, rd = ref.scann_search(h, q, k, nprobe, krefine)
+        assert rc == 0
+        oids, od = orc.scann_search(data, aniso, q, k, nprobe, krefine)
+        assert np.array_equal(oids, rids)
+        assert np.array_equal(_bits(od), _bits(rd))
+    ref.scann_destroy(h)
+    ref.destroy(inner)
+    ref.close()
