@@ -164,7 +164,11 @@ OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t inde
  * in device memory of the current HIP device: queries [nq*dim] f32, bitset
  * ((n+7)/8 bytes, may be NULL), neighbors [nq*k] i64, distances [nq*k] f32.
  * Returns after the results are complete. For callers that keep queries and
- * results resident in HBM (no PCIe copies on the search path). */
+ * results resident in HBM (no PCIe copies on the search path). The results are
+ * written in place by the search's last kernel: argument, limit and device
+ * errors leave neighbors and distances untouched, but OVVS_STATUS_ERROR from the
+ * search's own consistency checks (read after that kernel) may leave them
+ * written. */
 OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t index,
                                           const float* queries, int64_t nq, int64_t k,
                                           int32_t nprobe, int32_t krefine,

@@ -147,7 +147,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
     need += align256(static_cast<size_t>(nq) * 4);                        // shortlist counts
     need += align256(static_cast<size_t>(nq) * 16);                       // scan statistics
-    need += align256(nqk * 8) + align256(nqk * 4);                        // staged outputs
+    need += device_io ? 0 : align256(nqk * 8) + align256(nqk * 4);        // staged outputs
     need += align256(4 * 8);                                              // counters
     need += (!device_io && bitset) ? align256(bitset_bytes) : 0;
     SEARCH_TRY(res->reserve_workspace(need, work));
@@ -167,8 +167,10 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
     int32_t* d_scnt = cv.take<int32_t>(static_cast<size_t>(nq));
     int32_t* d_sstats = cv.take<int32_t>(static_cast<size_t>(nq) * 4);
-    int64_t* d_oid = cv.take<int64_t>(nqk);
-    float* d_odist = cv.take<float>(nqk);
+    // Device outputs are written by the refine kernel in place; host outputs are
+    // staged and copied only after the search has succeeded.
+    int64_t* d_oid = device_io ? neighbors : cv.take<int64_t>(nqk);
+    float* d_odist = device_io ? distances : cv.take<float>(nqk);
     unsigned long long* d_counters = cv.take<unsigned long long>(4);
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
     if (!device_io && bitset) {
@@ -322,13 +324,8 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // kernels count it instead of dereferencing it, and nothing is published.
     if (counters[3] != 0) return OVVS_STATUS_ERROR;
 
-    // Success: publish the outputs.
-    if (device_io) {
-      SEARCH_HIP(hipMemcpyAsync(neighbors, d_oid, nqk * 8, hipMemcpyDeviceToDevice, s));
-      SEARCH_HIP(hipMemcpyAsync(distances, d_odist, nqk * 4, hipMemcpyDeviceToDevice, s));
-      ovvs::saturating_add(work.wait_calls, 1);
-      SEARCH_HIP(hipStreamSynchronize(s));
-    } else {
+    // Success: publish the host outputs (device outputs already hold the results).
+    if (!device_io) {
       std::memcpy(neighbors, pin + 32, nqk * 8);
       std::memcpy(distances, pin + 32 + nqk * 8, nqk * 4);
     }

@@ -256,28 +256,43 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
   __syncthreads();
 
   // The P-th smallest group minimum of each row, bit by bit from the top: v is the
-  // smallest key with at least P group minima <= v. Each lane holds its slots.
+  // smallest key with at least P group minima <= v. Each lane holds its slots; the
+  // wave's rows are searched together (independent compare/count chains).
   const int ng = 16 * shape.nch;
-  for (int rr = 0; rr < kRowsPerWave; ++rr) {
-    const int row = kRowsPerWave * wave + rr;
-    uint32_t g[kMaxChunks / 4];
+  {
+    uint32_t g[kRowsPerWave][kMaxChunks / 4];
+    uint32_t v[kRowsPerWave];
 #pragma unroll
-    for (int i = 0; i < kMaxChunks / 4; ++i) {
-      const int s = lane + 64 * i;
-      g[i] = s < ng ? L.gmin[row * ng + s] : 0xffffffffu;
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int row = kRowsPerWave * wave + rr;
+#pragma unroll
+      for (int i = 0; i < kMaxChunks / 4; ++i) {
+        const int s = lane + 64 * i;
+        g[rr][i] = s < ng ? L.gmin[row * ng + s] : 0xffffffffu;
+      }
+      v[rr] = 0;
     }
-    uint32_t v = 0;
     for (int b = 31; b >= 0; --b) {
-      const uint32_t probe = v | ((1u << b) - 1u);
-      int cnt = 0;
+      int cnt[kRowsPerWave];
 #pragma unroll
-      for (int i = 0; i < kMaxChunks / 4; ++i) cnt += __popcll(__ballot(g[i] <= probe));
-      if (cnt < p.P) v |= 1u << b;
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const uint32_t probe = v[rr] | ((1u << b) - 1u);
+        cnt[rr] = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks / 4; ++i) cnt[rr] += __popcll(__ballot(g[rr][i] <= probe));
+      }
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr)
+        if (cnt[rr] < p.P) v[rr] |= 1u << b;
     }
     if (lane == 0) {
-      const int64_t q = q0 + row;
-      const float qnr = q < p.nq ? L.qn[row] : 0.f;
-      L.thr[row] = candidate_bound(key_to_score(v), qnr, p.cnorm_max, dim, KS);
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const int row = kRowsPerWave * wave + rr;
+        const int64_t q = q0 + row;
+        const float qnr = q < p.nq ? L.qn[row] : 0.f;
+        L.thr[row] = candidate_bound(key_to_score(v[rr]), qnr, p.cnorm_max, dim, KS);
+      }
     }
   }
   __syncthreads();
