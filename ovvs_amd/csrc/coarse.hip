@@ -214,16 +214,24 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
   return base + x - v;
 }
 
-__global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S, int64_t ldS,
-                                                     int N, int P, int M,
-                                                     const int32_t* __restrict__ flags,
-                                                     int32_t* __restrict__ out) {
-  extern __shared__ uint64_t sel[];  // [M]
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t scan_scratch[4];
-  __shared__ uint32_t s_digit, s_need;
-  const int64_t row = blockIdx.x;
-  if (flags && flags[row] == 0) return;  // uniform over the workgroup
+// LDS of one row selection.
+struct SelectLds {
+  uint64_t* sel;  // [M]
+  uint32_t* hist;
+  uint32_t* scan_scratch;
+  uint32_t* digit_need;  // [2]
+};
+
+// The first P columns of row `row` of S under the total order, in rank order, into
+// out[row * P ...]. Called by the whole workgroup.
+__device__ __forceinline__ void select_row(const float* __restrict__ S, int64_t ldS, int N, int P,
+                                           int M, int64_t row, int32_t* __restrict__ out,
+                                           const SelectLds& L) {
+  uint64_t* sel = L.sel;
+  uint32_t* hist = L.hist;
+  uint32_t* scan_scratch = L.scan_scratch;
+  uint32_t& s_digit = L.digit_need[0];
+  uint32_t& s_need = L.digit_need[1];
   const float* r = S + row * ldS;
 
   // 1. Radix select of the P-th smallest 32-bit score key.
@@ -290,6 +298,44 @@ __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S
   }
 }
 
+// Rows that flags marks (flags[row] != 0) among the workgroup's 256 rows
+// [256 * blockIdx.x, +256), compacted into rows[0, *count). Called by the whole
+// workgroup; a workgroup without flagged rows returns count 0 after one load.
+__device__ __forceinline__ int flagged_rows(const int32_t* __restrict__ flags, int64_t nrows,
+                                            int32_t* rows, int32_t* count) {
+  if (threadIdx.x == 0) *count = 0;
+  __syncthreads();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (row < nrows && flags[row] != 0) rows[atomicAdd(count, 1)] = static_cast<int32_t>(row);
+  __syncthreads();
+  return *count;
+}
+
+// flags == nullptr: one workgroup per row. Otherwise one workgroup per 256 rows,
+// selecting only the flagged ones (the rows the matrix-core probe could not
+// certify; usually none).
+__global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S, int64_t ldS,
+                                                     int N, int P, int M,
+                                                     const int32_t* __restrict__ flags,
+                                                     int64_t nrows, int32_t* __restrict__ out) {
+  extern __shared__ uint64_t sel[];  // [M]
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t scan_scratch[4];
+  __shared__ uint32_t digit_need[2];
+  __shared__ int32_t rows[256];
+  __shared__ int32_t count;
+  const SelectLds L{sel, hist, scan_scratch, digit_need};
+  if (!flags) {
+    select_row(S, ldS, N, P, M, blockIdx.x, out, L);
+    return;
+  }
+  const int n = flagged_rows(flags, nrows, rows, &count);
+  for (int i = 0; i < n; ++i) {
+    select_row(S, ldS, N, P, M, rows[i], out, L);
+    __syncthreads();  // sel is reused by the next row
+  }
+}
+
 }  // namespace
 
 extern "C" hipError_t ovvs_hip_row_norms(const float* x, int64_t n, int32_t dim, float* out,
@@ -338,8 +384,10 @@ extern "C" hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, 
     return hipErrorInvalidValue;
   int M = 1;
   while (M < P) M <<= 1;
-  hipLaunchKernelGGL(k_select_topk, dim3(static_cast<uint32_t>(nrows)), dim3(256),
-                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, flags, out);
+  const int64_t blocks = flags ? (nrows + 255) / 256 : nrows;
+  hipLaunchKernelGGL(k_select_topk, dim3(static_cast<uint32_t>(blocks)), dim3(256),
+                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, flags, nrows,
+                     out);
   return hipGetLastError();
 }
 

@@ -16,8 +16,9 @@
 //      b. query norms, exact coarse scores   ovvs_hip_row_norms, ovvs_hip_coarse_scores
 //         chunked over queries, row select   + ovvs_hip_select_topk
 //   2. the scan's query order                ovvs_hip_query_order
-//   3. fused LUT + code scan + shortlist    ovvs_hip_scan (+ ovvs_hip_scan_stats)
-//   4. exact re-rank + final select         ovvs_hip_refine
+//   3. fused LUT + code scan + shortlist    ovvs_hip_scan
+//   4. exact re-rank + final select, and    ovvs_hip_refine
+//      the sum of the scan's statistics
 // There is no host compute path: without a usable GPU the call fails with
 // OVVS_STATUS_DEVICE_UNAVAILABLE.
 #include <hip/hip_runtime_api.h>
@@ -281,7 +282,6 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.out_count = d_scnt;
     sa.out_stats = d_sstats;
     SEARCH_HIP(ovvs_hip_scan(&sa, s));
-    SEARCH_HIP(ovvs_hip_scan_stats(d_sstats, nq, d_counters, s));
     SEARCH_HIP(hipEventRecord(ev[3], s));
 
     OvvsRefineArgs ra{};
@@ -302,9 +302,11 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.out_ids = d_oid;
     ra.out_dist = d_odist;
     ra.invalid = d_counters + 3;
+    ra.stats = d_sstats;  // the scan's per-query statistics, summed by the same launch
+    ra.counters = d_counters;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += (mfma_probe ? 4 : 6) + 2 * chunks;
+    work.kernel_launches += (mfma_probe ? 3 : 5) + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

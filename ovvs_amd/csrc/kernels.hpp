@@ -172,10 +172,6 @@ hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, co
                                 int32_t nlist, int32_t* keys, int32_t keys_ready, int32_t* order,
                                 hipStream_t stream);
 int32_t ovvs_hip_query_key_shift(int32_t nlist);
-// counters[i] += sum over the queries of stats[q * 4 + i], i < 4 (the scan's
-// per-query statistics).
-hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq, unsigned long long* counters,
-                               hipStream_t stream);
 // Dynamic LDS bytes the scan kernel needs for these shapes, shortlist length and
 // probe count (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
 size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K,
@@ -199,6 +195,11 @@ struct OvvsRefineArgs {
   int64_t* out_ids;       // [nq * k]
   float* out_dist;        // [nq * k]
   unsigned long long* invalid;  // += shortlist entries whose position or id is out of range
+  // Optional (both or neither): counters[i] += sum over the queries of
+  // stats[q * 4 + i], i < 4 (the scan's per-query statistics), by extra
+  // workgroups of the same launch.
+  const int32_t* stats;
+  unsigned long long* counters;
 };
 
 // Exact re-rank of each query's shortlist by the index metric and final select

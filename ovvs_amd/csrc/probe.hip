@@ -364,18 +364,27 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
   }
 }
 
-// Exact scores of every centroid for the flagged queries (one workgroup per query;
-// unflagged queries return at once).
+// Exact scores of every centroid for the flagged queries: one workgroup per 256
+// queries, which scores its flagged ones (usually none: one load and return).
 __global__ __launch_bounds__(256) void k_probe_exact_rows(
-    const float* __restrict__ Q, const float* __restrict__ qn, const float* __restrict__ C,
-    const float* __restrict__ cn, int nlist, int dim, const int32_t* __restrict__ flags,
-    float* __restrict__ S) {
-  const int64_t q = blockIdx.x;
-  if (flags[q] == 0) return;
-  const float* qv = Q + q * dim;
-  const float qnq = qn[q];
-  for (int c = static_cast<int>(threadIdx.x); c < nlist; c += 256) {
-    S[q * nlist + c] = (qnq + cn[c]) - 2.f * seq_dot(qv, C + static_cast<int64_t>(c) * dim, dim);
+    const float* __restrict__ Q, const float* __restrict__ qn, int64_t nq,
+    const float* __restrict__ C, const float* __restrict__ cn, int nlist, int dim,
+    const int32_t* __restrict__ flags, float* __restrict__ S) {
+  __shared__ int32_t rows[256];
+  __shared__ int32_t count;
+  if (threadIdx.x == 0) count = 0;
+  __syncthreads();
+  const int64_t mine = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (mine < nq && flags[mine] != 0) rows[atomicAdd(&count, 1)] = static_cast<int32_t>(mine);
+  __syncthreads();
+  const int n = count;
+  for (int i = 0; i < n; ++i) {
+    const int64_t q = rows[i];
+    const float* qv = Q + q * dim;
+    const float qnq = qn[q];
+    for (int c = static_cast<int>(threadIdx.x); c < nlist; c += 256) {
+      S[q * nlist + c] = (qnq + cn[c]) - 2.f * seq_dot(qv, C + static_cast<int64_t>(c) * dim, dim);
+    }
   }
 }
 
@@ -488,7 +497,7 @@ extern "C" hipError_t ovvs_hip_probe_exact_rows(const float* Q, const float* qn,
   if (nq <= 0) return hipSuccess;
   if (!Q || !qn || !C || !cn || !flags || !S || nlist <= 0 || dim <= 0 || nq > 0x7fffffff)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_probe_exact_rows, dim3(static_cast<uint32_t>(nq)), dim3(256), 0, stream,
-                     Q, qn, C, cn, nlist, dim, flags, S);
+  hipLaunchKernelGGL(k_probe_exact_rows, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256), 0,
+                     stream, Q, qn, nq, C, cn, nlist, dim, flags, S);
   return hipGetLastError();
 }

@@ -7,12 +7,15 @@
 // (distance, shortlist rank), flip the sign back for inner product, and pad the
 // remaining slots with (-1, +inf).
 //
-// One wave64 per query: the query row is staged in LDS, each lane scores
+// One wave64 per query (plus, when asked, up to 64 workgroups that sum the scan's
+// per-query statistics into the search counters): the query row is staged in LDS, each lane scores
 // shortlist entries i = lane, lane+64, ... with left-to-right fp32 sums (rows
 // read 16 bytes at a time when dim % 4 == 0), the (key, rank) pairs are sorted in
 // LDS by a single-wave bitonic network, and the first k slots are written. LDS is
 // sized to the shortlist (a power of two >= krefine), so short shortlists keep
 // many waves resident.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -78,7 +81,31 @@ size_t refine_lds(int dim, int M) {
   return align16(static_cast<size_t>((dim + 3) & ~3) * 4) + static_cast<size_t>(M) * 12;
 }
 
+// Workgroups past the queries sum the scan's per-query statistics (a wave each,
+// strided over the queries, one atomic per counter and workgroup).
+__device__ void refine_stats(const OvvsRefineArgs& a, int64_t g, int64_t ng) {
+  unsigned long long acc[4] = {0, 0, 0, 0};
+  for (int64_t q = g * 64 + threadIdx.x; q < a.nq; q += ng * 64) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += static_cast<uint32_t>(a.stats[q * 4 + i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc[i] += shfl_xor_u64(acc[i], o);
+  }
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (acc[i]) atomicAdd(&a.counters[i], acc[i]);
+  }
+}
+
 __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
+  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
+    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
+    return;
+  }
   extern __shared__ __align__(16) unsigned char smem[];
   float* qs = reinterpret_cast<float*>(smem);
   uint64_t* keys =
@@ -151,7 +178,8 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
       !a.short_count || !a.out_ids || !a.out_dist || !a.invalid || a.n <= 0 || a.positions <= 0 ||
       a.dim <= 0 ||
       a.K <= 0 ||
-      a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff)
+      a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff - 64 ||
+      (a.stats == nullptr) != (a.counters == nullptr))
     return hipErrorInvalidValue;
   int M = 1;
   while (M < a.K) M <<= 1;
@@ -163,6 +191,8 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
                                              static_cast<int>(lds));
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq)), dim3(64), lds, stream, a, M);
+  const int64_t stat_groups = a.stats ? std::min<int64_t>(64, (a.nq + 63) / 64) : 0;
+  hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq + stat_groups)), dim3(64), lds,
+                     stream, a, M);
   return hipGetLastError();
 }

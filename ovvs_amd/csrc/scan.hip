@@ -1211,8 +1211,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
     if (lane == 0) {
       a.out_count[q] = valid;
-      // Per-query statistics, summed by ovvs_hip_scan_stats (no atomics here:
-      // tens of thousands of workgroups adding into one address serialize).
+      // Per-query statistics, summed by the statistics workgroups of the refine
+      // launch (no atomics here: tens of thousands of workgroups adding into one
+      // address serialize).
       a.out_stats[q * 4 + 0] = misc[2];
       a.out_stats[q * 4 + 1] = misc[3];
       a.out_stats[q * 4 + 2] = valid;
@@ -1314,33 +1315,6 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   }
 }
 
-namespace {
-
-__global__ __launch_bounds__(256) void k_scan_stats(const int32_t* __restrict__ stats, int64_t nq,
-                                                   unsigned long long* __restrict__ counters) {
-  unsigned long long acc[4] = {0, 0, 0, 0};
-  for (int64_t q = blockIdx.x * 256ll + threadIdx.x; q < nq; q += static_cast<int64_t>(gridDim.x) * 256) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += static_cast<uint32_t>(stats[q * 4 + i]);
-  }
-  __shared__ unsigned long long part[4][4];
-  const int lane = lane_id(), wave = static_cast<int>(threadIdx.x >> 6);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc[i] += shfl_xor_u64(acc[i], o);
-    if (lane == 0) part[wave][i] = acc[i];
-  }
-  __syncthreads();
-  if (threadIdx.x < 4) {
-    const unsigned long long v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] +
-                                 part[3][threadIdx.x];
-    if (v) atomicAdd(&counters[threadIdx.x], v);
-  }
-}
-
-}  // namespace
-
 // Bucket of every query: the spatial rank of its nearest probed list, shifted to at
 // most 4096 buckets (bucket 0 for an invalid probe id).
 __global__ __launch_bounds__(256) void k_query_keys(const int32_t* __restrict__ probes, int64_t nq, int P,
@@ -1355,15 +1329,31 @@ __global__ __launch_bounds__(256) void k_query_keys(const int32_t* __restrict__ 
 
 // Counting sort of the queries by bucket; one workgroup, LDS counters.
 constexpr int kOrderThreads = 1024;
+constexpr int kOrderKeys = 16;  // keys per thread held in registers
 __global__ __launch_bounds__(kOrderThreads) void k_query_order(const int32_t* __restrict__ keys, int64_t nq,
                                                                int32_t* __restrict__ order) {
   __shared__ int32_t hist[4096];
   __shared__ int32_t wsum[kOrderThreads / 64];
   const int t = static_cast<int>(threadIdx.x);
   const int lane = lane_id(), wave = t >> 6;
+  // Batches of kOrderKeys keys stay in registers between the count and the
+  // placement when the batch holds them all (nq <= kOrderKeys * kOrderThreads).
+  const bool held = nq <= static_cast<int64_t>(kOrderKeys) * kOrderThreads;
+  int32_t kv[kOrderKeys];
+#pragma unroll
+  for (int j = 0; j < kOrderKeys; ++j) {
+    const int64_t q = t + static_cast<int64_t>(j) * kOrderThreads;
+    kv[j] = held && q < nq ? keys[q] : -1;
+  }
   for (int i = t; i < 4096; i += kOrderThreads) hist[i] = 0;
   __syncthreads();
-  for (int64_t q = t; q < nq; q += kOrderThreads) atomicAdd(&hist[keys[q]], 1);
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kOrderKeys; ++j)
+      if (kv[j] >= 0) atomicAdd(&hist[kv[j]], 1);
+  } else {
+    for (int64_t q = t; q < nq; q += kOrderThreads) atomicAdd(&hist[keys[q]], 1);
+  }
   __syncthreads();
   // Exclusive prefix sums of the 4096 counters: four per thread, then across the
   // lanes of each wave and across the 16 waves.
@@ -1386,7 +1376,13 @@ __global__ __launch_bounds__(kOrderThreads) void k_query_order(const int32_t* __
     base += c[i];
   }
   __syncthreads();
-  for (int64_t q = t; q < nq; q += kOrderThreads) order[atomicAdd(&hist[keys[q]], 1)] = static_cast<int32_t>(q);
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kOrderKeys; ++j)
+      if (kv[j] >= 0) order[atomicAdd(&hist[kv[j]], 1)] = t + j * kOrderThreads;
+  } else {
+    for (int64_t q = t; q < nq; q += kOrderThreads) order[atomicAdd(&hist[keys[q]], 1)] = static_cast<int32_t>(q);
+  }
 }
 
 extern "C" int32_t ovvs_hip_query_key_shift(int32_t nlist) {
@@ -1410,12 +1406,3 @@ extern "C" hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, in
   return hipGetLastError();
 }
 
-extern "C" hipError_t ovvs_hip_scan_stats(const int32_t* stats, int64_t nq,
-                                          unsigned long long* counters, hipStream_t stream) {
-  if (nq <= 0) return hipSuccess;
-  if (!stats || !counters) return hipErrorInvalidValue;
-  const int64_t blocks = (nq + 255) / 256;
-  hipLaunchKernelGGL(k_scan_stats, dim3(static_cast<uint32_t>(blocks < 64 ? blocks : 64)), dim3(256),
-                     0, stream, stats, nq, counters);
-  return hipGetLastError();
-}
