@@ -311,13 +311,25 @@ __device__ __forceinline__ int flagged_rows(const int32_t* __restrict__ flags, i
   return *count;
 }
 
-// flags == nullptr: one workgroup per row. Otherwise one workgroup per 256 rows,
-// selecting only the flagged ones (the rows the matrix-core probe could not
-// certify; usually none).
+// One workgroup per row.
 __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S, int64_t ldS,
                                                      int N, int P, int M,
-                                                     const int32_t* __restrict__ flags,
-                                                     int64_t nrows, int32_t* __restrict__ out) {
+                                                     int32_t* __restrict__ out) {
+  extern __shared__ uint64_t sel[];  // [M]
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t scan_scratch[4];
+  __shared__ uint32_t digit_need[2];
+  select_row(S, ldS, N, P, M, blockIdx.x, out, SelectLds{sel, hist, scan_scratch, digit_need});
+}
+
+// The exact route for the queries the matrix-core probe flagged (usually none):
+// one workgroup per 256 queries; for each flagged one, the exact score of every
+// centroid into its row of S, then the row selection.
+__global__ __launch_bounds__(256) void k_probe_fallback(
+    const float* __restrict__ Q, const float* __restrict__ qn, int64_t nq,
+    const float* __restrict__ C, const float* __restrict__ cn, int nlist, int dim,
+    const int32_t* __restrict__ flags, float* __restrict__ S, int P, int M,
+    int32_t* __restrict__ out) {
   extern __shared__ uint64_t sel[];  // [M]
   __shared__ uint32_t hist[256];
   __shared__ uint32_t scan_scratch[4];
@@ -325,13 +337,16 @@ __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S
   __shared__ int32_t rows[256];
   __shared__ int32_t count;
   const SelectLds L{sel, hist, scan_scratch, digit_need};
-  if (!flags) {
-    select_row(S, ldS, N, P, M, blockIdx.x, out, L);
-    return;
-  }
-  const int n = flagged_rows(flags, nrows, rows, &count);
+  const int n = flagged_rows(flags, nq, rows, &count);
   for (int i = 0; i < n; ++i) {
-    select_row(S, ldS, N, P, M, rows[i], out, L);
+    const int64_t q = rows[i];
+    const float* qv = Q + q * dim;
+    const float qnq = qn[q];
+    for (int c = static_cast<int>(threadIdx.x); c < nlist; c += 256) {
+      S[q * nlist + c] = (qnq + cn[c]) - 2.f * seq_dot(qv, C + static_cast<int64_t>(c) * dim, dim);
+    }
+    __syncthreads();  // the row of S is complete (workgroup-scope release/acquire)
+    select_row(S, nlist, nlist, P, M, q, out, L);
     __syncthreads();  // sel is reused by the next row
   }
 }
@@ -375,23 +390,31 @@ extern "C" hipError_t ovvs_hip_coarse_argmin(const float* Q, const float* qn, in
   return hipGetLastError();
 }
 
-extern "C" hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nrows,
-                                                   int32_t N, int32_t P, const int32_t* flags,
-                                                   int32_t* out, hipStream_t stream) {
+extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N,
+                                           int32_t P, int32_t* out, hipStream_t stream) {
   if (nrows <= 0) return hipSuccess;
   if (!S || !out || N <= 0 || P <= 0 || P > N || P > OVVS_HIP_MAX_PROBES || ldS < N ||
       nrows > 0x7fffffff)
     return hipErrorInvalidValue;
   int M = 1;
   while (M < P) M <<= 1;
-  const int64_t blocks = flags ? (nrows + 255) / 256 : nrows;
-  hipLaunchKernelGGL(k_select_topk, dim3(static_cast<uint32_t>(blocks)), dim3(256),
-                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, flags, nrows,
-                     out);
+  hipLaunchKernelGGL(k_select_topk, dim3(static_cast<uint32_t>(nrows)), dim3(256),
+                     static_cast<size_t>(M) * sizeof(uint64_t), stream, S, ldS, N, P, M, out);
   return hipGetLastError();
 }
 
-extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N,
-                                           int32_t P, int32_t* out, hipStream_t stream) {
-  return ovvs_hip_select_topk_flagged(S, ldS, nrows, N, P, nullptr, out, stream);
+extern "C" hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, int64_t nq,
+                                              const float* C, const float* cn, int32_t nlist,
+                                              int32_t dim, const int32_t* flags, float* S,
+                                              int32_t P, int32_t* out, hipStream_t stream) {
+  if (nq <= 0) return hipSuccess;
+  if (!Q || !qn || !C || !cn || !flags || !S || !out || nlist <= 0 || dim <= 0 || P <= 0 ||
+      P > nlist || P > OVVS_HIP_MAX_PROBES || nq > 0x7fffffff)
+    return hipErrorInvalidValue;
+  int M = 1;
+  while (M < P) M <<= 1;
+  hipLaunchKernelGGL(k_probe_fallback, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256),
+                     static_cast<size_t>(M) * sizeof(uint64_t), stream, Q, qn, nq, C, cn, nlist,
+                     dim, flags, S, P, M, out);
+  return hipGetLastError();
 }

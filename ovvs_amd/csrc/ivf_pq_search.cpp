@@ -11,8 +11,7 @@
 //      a. matrix-core probe with exact       ovvs_hip_probe_mfma (it also computes the
 //         re-score (dim <= 128, enough        query norms and clears the counters), then
 //         centroid groups)                    for the queries it flags
-//                                             ovvs_hip_probe_exact_rows +
-//                                             ovvs_hip_select_topk_flagged
+//                                             ovvs_hip_probe_fallback
 //      b. query norms, exact coarse scores   ovvs_hip_row_norms, ovvs_hip_coarse_scores
 //         chunked over queries, row select   + ovvs_hip_select_topk
 //   2. the scan's query order                ovvs_hip_query_order
@@ -220,11 +219,10 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       SEARCH_HIP(hipEventRecord(ev[1], s));
       for (int64_t q0 = 0; q0 < nq; q0 += qc) {
         const int64_t cnt = std::min(qc, nq - q0);
-        SEARCH_HIP(ovvs_hip_probe_exact_rows(d_q + q0 * dim, d_qn + q0, cnt,
-                                             dv.centroids.as<float>(), dv.cnorm.as<float>(),
-                                             ix.nlist, dim, d_flags + q0, d_scores, s));
-        SEARCH_HIP(ovvs_hip_select_topk_flagged(d_scores, ix.nlist, cnt, ix.nlist, P,
-                                                d_flags + q0, d_probes + q0 * P, s));
+        SEARCH_HIP(ovvs_hip_probe_fallback(d_q + q0 * dim, d_qn + q0, cnt,
+                                           dv.centroids.as<float>(), dv.cnorm.as<float>(),
+                                           ix.nlist, dim, d_flags + q0, d_scores, P,
+                                           d_probes + q0 * P, s));
         ++chunks;
       }
       work.kernel_launches += 1;
@@ -306,7 +304,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.counters = d_counters;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += (mfma_probe ? 3 : 5) + 2 * chunks;
+    work.kernel_launches += mfma_probe ? 3 + chunks : 5 + 2 * chunks;
 
     unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));

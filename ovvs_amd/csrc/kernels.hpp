@@ -56,10 +56,6 @@ hipError_t ovvs_hip_coarse_scores(const float* Q, const float* qn, int64_t nq, c
 // out[row*P + r] (reference cpu_prims.cpp:24-106). P <= OVVS_HIP_MAX_PROBES, P <= N.
 hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N, int32_t P,
                                 int32_t* out, hipStream_t stream);
-// The same for the rows with flags[row] != 0 only; other rows are left untouched.
-hipError_t ovvs_hip_select_topk_flagged(const float* S, int64_t ldS, int64_t nrows, int32_t N,
-                                        int32_t P, const int32_t* flags, int32_t* out,
-                                        hipStream_t stream);
 
 // ---- coarse probe on the fp32 matrix cores (probe.hip) ----
 
@@ -106,10 +102,14 @@ size_t ovvs_hip_probe_cmfma_words(int32_t dim, int32_t nlist);
 void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, uint32_t* out);
 // Probe selection for every query; flags the queries the exact route must finish.
 hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream);
-// Exact coarse scores S[q*nlist + c] of every centroid, for flagged queries only.
-hipError_t ovvs_hip_probe_exact_rows(const float* Q, const float* qn, int64_t nq, const float* C,
-                                     const float* cn, int32_t nlist, int32_t dim,
-                                     const int32_t* flags, float* S, hipStream_t stream);
+// The exact route for the queries with flags[q] != 0 (the ones the fused probe could
+// not certify): exact scores of every centroid into S[q*nlist + c] (a scratch of
+// nq * nlist floats), then their first P centroids in rank order into out[q*P ...].
+// Unflagged queries are left untouched.
+hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, int64_t nq, const float* C,
+                                   const float* cn, int32_t nlist, int32_t dim,
+                                   const int32_t* flags, float* S, int32_t P, int32_t* out,
+                                   hipStream_t stream);
 
 // Exact argmin over all centroids for each row of Q (top-1 of the coarse score
 // under the same total order), fused with the score computation: labels[i].

@@ -35,9 +35,8 @@
 //            its rank is the number of candidates with a smaller (s, c) key, and the
 //            P of rank < P are the probes in order, bit for bit.
 // A query with more candidates than the re-score capacity, or fewer than P (only NaN
-// or infinite inputs can cause that), is flagged in `fallback`; k_probe_exact_rows and
-// the flagged row selection of coarse.hip then rank it from exact scores of every
-// centroid.
+// or infinite inputs can cause that), is flagged in `fallback`; k_probe_fallback
+// (coarse.hip) then ranks it from exact scores of every centroid.
 #include <cstring>
 
 #include "device_common.hpp"
@@ -364,30 +363,6 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
   }
 }
 
-// Exact scores of every centroid for the flagged queries: one workgroup per 256
-// queries, which scores its flagged ones (usually none: one load and return).
-__global__ __launch_bounds__(256) void k_probe_exact_rows(
-    const float* __restrict__ Q, const float* __restrict__ qn, int64_t nq,
-    const float* __restrict__ C, const float* __restrict__ cn, int nlist, int dim,
-    const int32_t* __restrict__ flags, float* __restrict__ S) {
-  __shared__ int32_t rows[256];
-  __shared__ int32_t count;
-  if (threadIdx.x == 0) count = 0;
-  __syncthreads();
-  const int64_t mine = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (mine < nq && flags[mine] != 0) rows[atomicAdd(&count, 1)] = static_cast<int32_t>(mine);
-  __syncthreads();
-  const int n = count;
-  for (int i = 0; i < n; ++i) {
-    const int64_t q = rows[i];
-    const float* qv = Q + q * dim;
-    const float qnq = qn[q];
-    for (int c = static_cast<int>(threadIdx.x); c < nlist; c += 256) {
-      S[q * nlist + c] = (qnq + cn[c]) - 2.f * seq_dot(qv, C + static_cast<int64_t>(c) * dim, dim);
-    }
-  }
-}
-
 // Shape of a launch, or false when the fused probe does not serve these sizes.
 bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
   if (dim <= 0 || dim > 32 * OVVS_PROBE_MAX_KSTEPS || nlist <= 0 || nlist > (1 << 24) || P <= 0 ||
@@ -488,16 +463,4 @@ extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t
     case 3: return launch_probe<3>(p, sh, stream);
     default: return launch_probe<4>(p, sh, stream);
   }
-}
-
-extern "C" hipError_t ovvs_hip_probe_exact_rows(const float* Q, const float* qn, int64_t nq,
-                                                const float* C, const float* cn, int32_t nlist,
-                                                int32_t dim, const int32_t* flags, float* S,
-                                                hipStream_t stream) {
-  if (nq <= 0) return hipSuccess;
-  if (!Q || !qn || !C || !cn || !flags || !S || nlist <= 0 || dim <= 0 || nq > 0x7fffffff)
-    return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_probe_exact_rows, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256), 0,
-                     stream, Q, qn, nq, C, cn, nlist, dim, flags, S);
-  return hipGetLastError();
 }
