@@ -70,6 +70,55 @@ __device__ __forceinline__ float seq_dot_v4(const float* __restrict__ q,
   return s;
 }
 
+// seq_dot_v4 with the row x (global memory) double-buffered: the next four
+// vectors are requested before the current four are summed, so one memory round
+// trip overlaps the next. q is read from LDS as it is consumed. Same sum, same
+// order.
+__device__ __forceinline__ float seq_dot_v4_ahead(const float* __restrict__ q,
+                                                  const float* __restrict__ x, int d) {
+  const float4* q4 = reinterpret_cast<const float4*>(q);
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const int n4 = d / 4;
+  float s = 0.f;
+  int i = 0;
+  if (n4 >= 4) {
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = x4[j];
+    for (i = 4; i + 4 <= n4; i += 4) {
+      float4 nv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nv[j] = x4[i + j];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 w = q4[i - 4 + j];
+        s = s + w.x * v[j].x;
+        s = s + w.y * v[j].y;
+        s = s + w.z * v[j].z;
+        s = s + w.w * v[j].w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = nv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 w = q4[i - 4 + j];
+      s = s + w.x * v[j].x;
+      s = s + w.y * v[j].y;
+      s = s + w.z * v[j].z;
+      s = s + w.w * v[j].w;
+    }
+  }
+  for (; i < n4; ++i) {
+    const float4 v = x4[i], w = q4[i];
+    s = s + w.x * v.x;
+    s = s + w.y * v.y;
+    s = s + w.z * v.z;
+    s = s + w.w * v.w;
+  }
+  return s;
+}
+
 __device__ __forceinline__ float seq_l2sq(const float* a, const float* b, int d) {
   float s = 0.f;
   for (int i = 0; i < d; ++i) {

@@ -345,7 +345,7 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     const uint32_t c = static_cast<uint32_t>(*s);
     const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
     const float* qrow = L.qs + row * dq;
-    const float dot = (dim & 3) == 0 ? seq_dot_v4(qrow, crow, dim) : seq_dot(qrow, crow, dim);
+    const float dot = (dim & 3) == 0 ? seq_dot_v4_ahead(qrow, crow, dim) : seq_dot(qrow, crow, dim);
     *s = make_key((L.qn[row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();
