@@ -15,6 +15,9 @@
 //   k_select_topk    one workgroup per query row: 4-pass 8-bit radix select of the
 //                    P-th smallest score key, ordered compaction of the winners,
 //                    bitonic sort of (key, column) in LDS.
+//   k_probe_fallback the exact route for the queries the matrix-core probe flags:
+//                    one workgroup per 256 queries, each flagged one scored against
+//                    every centroid and selected as in k_select_topk.
 //   k_coarse_argmin  the GEMM tile loop over all centroids for 64 rows with a
 //                    running (key, column) minimum: the k-means / extend assignment.
 #include "device_common.hpp"
