@@ -173,9 +173,10 @@ class Resources:
         _check_status(_lib.ovvsResourcesCreate(ctypes.byref(self._h)), "ovvsResourcesCreate")
 
     def close(self):
-        if self._h:
+        # At interpreter exit the module's globals may already be cleared.
+        if self._h and _lib is not None:
             _lib.ovvsResourcesDestroy(self._h)
-            self._h = None
+        self._h = None
 
     def __del__(self):
         self.close()
@@ -252,9 +253,9 @@ class IvfPqIndex:
         self._own = own_res
 
     def close(self):
-        if self._h:
+        if self._h and _lib is not None:
             _lib.ovvsIvfPqDestroy(self._h)
-            self._h = None
+        self._h = None
         if self._own and self._res is not None:
             self._res.close()
             self._res = None
@@ -321,9 +322,9 @@ class ScannIndex:
         self._own = own_res
 
     def close(self):
-        if self._h:
+        if self._h and _lib is not None:
             _lib.ovvsScannDestroy(self._h)
-            self._h = None
+        self._h = None
         if self._own and self._res is not None:
             self._res.close()
             self._res = None
