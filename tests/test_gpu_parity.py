@@ -256,6 +256,32 @@ def test_many_groups_and_odd_batches_against_oracle(ovvs, res, tmp_path):
     ix.close()
 
 
+def test_limits_against_oracle(ovvs, res, tmp_path):
+    """The largest shortlist the kernels hold (krefine = k = 1024, more than the
+    probed rows: -1 / +inf padding) and probe counts in the thousands (2048 of 2048
+    lists, nprobe 4096 clamped to nlist), bit-identical to the oracle."""
+    rng = np.random.default_rng(23)
+    n, dim, nlist = 30000, 16, 2048
+    centers = rng.standard_normal((64, dim)).astype(np.float32)
+    data = (centers[rng.integers(0, 64, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    q = (centers[rng.integers(0, 64, 20)] + 0.3 * rng.standard_normal((20, dim))).astype(np.float32)
+    say("limits build", n, dim, nlist)
+    ix = ovvs.neighbors.ivf_pq.build(data, metric=0, nlist=nlist, pq_m=4, pq_nbits=8, resources=res)
+    p = tmp_path / "limits.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for k, nprobe, krefine in [(1024, 64, 1024), (10, 2048, 10), (100, 4096, 1000), (5, 1500, 1024)]:
+        say("limits search", k, nprobe, krefine)
+        ids, d = ix.search(q, k, nprobe, krefine)
+        oids, od = orc.search(q, k, nprobe, krefine)
+        assert np.array_equal(ids, oids), (k, nprobe, krefine)
+        assert np.array_equal(_bits(d), _bits(od)), (k, nprobe, krefine)
+        if k == 1024 and nprobe == 64:
+            # 64 lists of about 15 rows: the padded tail is part of what was compared.
+            assert np.any(oids[:, -1] == -1)
+    ix.close()
+
+
 def test_device_pointer_entry_matches_host_entry(ovvs, res, ref_cases, tmp_path):
     import torch
 
