@@ -7,8 +7,9 @@
 // (distance, shortlist rank), flip the sign back for inner product, and pad the
 // remaining slots with (-1, +inf).
 //
-// One wave64 per query (plus, when asked, up to 64 workgroups that sum the scan's
-// per-query statistics into the search counters): the query row is staged in LDS, each lane scores
+// One wave64 per query, or four per wave for shortlists of at most 16 (plus, when
+// asked, up to 64 workgroups that sum the scan's per-query statistics into the
+// search counters): the query row is staged in LDS, each lane scores
 // shortlist entries i = lane, lane+64, ... with left-to-right fp32 sums (rows
 // read 16 bytes at a time when dim % 4 == 0), the (key, rank) pairs are sorted in
 // LDS by a single-wave bitonic network, and the first k slots are written. LDS is
@@ -168,6 +169,83 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax)
   }
 }
 
+// Shortlists of at most 16 (M <= 16): four queries per wave64, 16 lanes each, so a
+// batch needs a quarter of the waves. Lane i of a group scores entry i; the 16 keys
+// of each group are sorted by the same bitonic network in LDS.
+constexpr int kGroupLanes = 16;
+constexpr int kGroups = 64 / kGroupLanes;
+
+size_t refine4_lds(int dim) {
+  return align16(static_cast<size_t>(kGroups) * ((dim + 3) & ~3) * 4) +
+         static_cast<size_t>(64) * 12;
+}
+
+__global__ __launch_bounds__(64) void k_refine4(const OvvsRefineArgs a) {
+  const int64_t nblk = (a.nq + kGroups - 1) / kGroups;
+  if (static_cast<int64_t>(blockIdx.x) >= nblk) {
+    refine_stats(a, blockIdx.x - nblk, gridDim.x - nblk);
+    return;
+  }
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int dq = (a.dim + 3) & ~3;
+  float* qs_all = reinterpret_cast<float*>(smem);
+  uint64_t* keys_all =
+      reinterpret_cast<uint64_t*>(smem + align16(static_cast<size_t>(kGroups) * dq * 4));
+  float* vals_all = reinterpret_cast<float*>(keys_all + 64);
+  const int lane = threadIdx.x;
+  const int grp = lane / kGroupLanes, i = lane % kGroupLanes;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kGroups + grp;
+  const bool qok = q < a.nq;
+  float* qs = qs_all + grp * dq;
+  uint64_t* keys = keys_all + grp * kGroupLanes;
+  float* vals = vals_all + grp * kGroupLanes;
+  for (int t = i; t < a.dim; t += kGroupLanes) qs[t] = qok ? a.queries[q * a.dim + t] : 0.f;
+  __syncthreads();
+  int cnt = qok ? a.short_count[q] : 0;
+  cnt = cnt < 0 ? 0 : (cnt > a.K ? a.K : cnt);
+  uint64_t key = kNoKey;
+  if (i < cnt) {
+    const int32_t pos = a.short_pos[q * a.K + i];
+    const int64_t id = (pos >= 0 && pos < a.positions) ? a.ids[pos] : -1;
+    if (id >= 0 && id < a.n) {
+      const float v = metric_value(a.metric, qs, a.dataset + id * a.dim, a.dim, a.qnorm[q],
+                                   a.xnorm[id]);
+      key = make_key(v, static_cast<uint32_t>(i));
+      vals[i] = v;
+    } else {
+      atomicAdd(a.invalid, 1ull);
+    }
+  }
+  keys[i] = key;
+  __syncthreads();
+  for (int k = 2; k <= kGroupLanes; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int p = i ^ j;
+      if (p > i) {
+        const uint64_t x = keys[i], y = keys[p];
+        if ((x > y) == ((i & k) == 0)) {
+          keys[i] = y;
+          keys[p] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (!qok) return;
+  const int64_t kk = a.k < cnt ? a.k : cnt;
+  for (int64_t t = i; t < a.k; t += kGroupLanes) {
+    int64_t id = -1;
+    float d = __builtin_inff();
+    if (t < kk && keys[t] != kNoKey) {
+      const int e = static_cast<int>(keys[t] & 0xffffffffu);
+      id = a.ids[a.short_pos[q * a.K + e]];
+      d = a.metric == kIP ? -vals[e] : vals[e];
+    }
+    a.out_ids[q * a.k + t] = id;
+    a.out_dist[q * a.k + t] = d;
+  }
+}
+
 }  // namespace
 
 extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream) {
@@ -183,6 +261,15 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
     return hipErrorInvalidValue;
   int M = 1;
   while (M < a.K) M <<= 1;
+  const int64_t stat_groups = a.stats ? std::min<int64_t>(64, (a.nq + 63) / 64) : 0;
+  if (M <= kGroupLanes) {
+    const size_t lds4 = refine4_lds(a.dim);
+    if (lds4 <= 65536) {
+      const int64_t blocks = (a.nq + kGroups - 1) / kGroups + stat_groups;
+      hipLaunchKernelGGL(k_refine4, dim3(static_cast<uint32_t>(blocks)), dim3(64), lds4, stream, a);
+      return hipGetLastError();
+    }
+  }
   const size_t lds = refine_lds(a.dim, M);
   if (lds > 160u * 1024u) return hipErrorInvalidValue;
   if (lds > 65536) {
@@ -191,7 +278,6 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
                                              static_cast<int>(lds));
     if (e != hipSuccess) return e;
   }
-  const int64_t stat_groups = a.stats ? std::min<int64_t>(64, (a.nq + 63) / 64) : 0;
   hipLaunchKernelGGL(k_refine, dim3(static_cast<uint32_t>(a.nq + stat_groups)), dim3(64), lds,
                      stream, a, M);
   return hipGetLastError();
