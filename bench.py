@@ -252,7 +252,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU; "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+              "multi-GPU sharding is a design, not built", file=sys.stderr)
         return 2
 
     import torch
