@@ -175,6 +175,21 @@ OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t 
                                           const uint8_t* bitset, ovvsDType lut_dtype,
                                           int64_t* neighbors, float* distances);
 
+/* ADDITIVE (the reference computes this inside its CAGRA build: the IVF-PQ
+ * initializer, reference src/neighbors/graphs.cpp:767-797, with no entry point of its
+ * own). The k-nearest-neighbour graph of the rows by IVF-PQ: an index is built with
+ * ovvsIvfPqBuild(nlist = max(2, min(8, n/4)), pq_m = the largest divisor of dim not
+ * above 4, 8-bit codes), every row is searched with k = krefine = degree + 1 and every
+ * list probed, and graph[i * degree ...] (int32, caller-allocated, n * degree) holds
+ * row i's results other than i itself and -1, in rank order, padded with -1. The rows'
+ * searches run as batches (each batch is one IVF-PQ search in the telemetry); the
+ * index is destroyed before returning. degree < 0 is INVALID_ARGUMENT, degree >= 1024
+ * DEVICE_UNAVAILABLE (the search's shortlist limit); the build's statuses pass through.
+ * graph is untouched on failure. */
+OVVS_API ovvsStatus ovvsIvfPqKnnGraph(ovvsResources_t res, const float* dataset, int64_t n,
+                                      int64_t dim, ovvsMetric metric, int32_t degree,
+                                      int32_t* graph);
+
 /* ScaNN-style index: IVF-PQ trained on column-scaled rows, re-ranked in the
  * original space (reference include/ovvs/ovvs.h:393-399,
  * src/neighbors/graphs.cpp:3286-3385).

@@ -127,6 +127,8 @@ _SIGS = {
     "ovvsScannSearch": (c_int32, [_V, _V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
                                   POINTER(c_int64), POINTER(c_float)]),
     "ovvsScannDestroy": (c_int32, [_V]),
+    "ovvsIvfPqKnnGraph": (c_int32, [_V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
+                                    POINTER(c_int32)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -374,6 +376,20 @@ class neighbors:
                                      ctypes.byref(h))
             _check_status(rc, "IVF-PQ build")
             return IvfPqIndex(res, h, x.shape[1], own_res=resources is None, n=x.shape[0])
+
+        @staticmethod
+        def knn_graph(dataset, degree, dim=None, metric=0, resources=None):
+            """k-nearest-neighbour graph [n, degree] int32 of the rows by IVF-PQ (the
+            CAGRA build's IVF-PQ initializer, reference src/neighbors/graphs.cpp:767-797)."""
+            res = resources or Resources()
+            x = _f32_matrix(dataset, dim)
+            g = np.empty((x.shape[0], int(degree)), dtype=np.int32)
+            rc = _lib.ovvsIvfPqKnnGraph(res._h, x.ctypes.data_as(POINTER(c_float)),
+                                        c_int64(x.shape[0]), c_int64(x.shape[1]),
+                                        c_int32(metric), c_int32(degree),
+                                        g.ctypes.data_as(POINTER(c_int32)))
+            _check_status(rc, "IVF-PQ knn graph")
+            return g
 
         @staticmethod
         def load(path, resources=None):

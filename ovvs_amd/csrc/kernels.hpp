@@ -207,6 +207,13 @@ struct OvvsRefineArgs {
 // inner-product distances are returned as +ip (reference indexes.cpp:1067-1096).
 hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream);
 
+// IVF-PQ k-nearest-neighbour graph (reference src/neighbors/graphs.cpp:767-797): for
+// rows row0 + r, r < n, with search results nb[r * (degree + 1) ...] (rank order),
+// graph[(row0 + r) * degree ...] = the results other than the row itself and -1, at
+// most degree of them, then -1.
+hipError_t ovvs_hip_knn_graph_rows(const int64_t* nb, int64_t n, int64_t row0, int32_t degree,
+                                   int32_t* graph, hipStream_t stream);
+
 // ScaNN-style index (reference src/neighbors/graphs.cpp:3286-3374).
 // aniso[d] = sqrt(var_d / max(n, 1) + 1e-6) from left-to-right fp32 column sums
 // (mean = sum / n, then var_d = sum of (x - mean)^2); one thread per column.

@@ -304,3 +304,27 @@ def test_scann_build_without_gpu_is_device_unavailable(ovvs):
     rc = ovvs._lib.ovvsScannBuild(res._h, x.ctypes.data_as(POINTER(c_float)), 16, 4, 0, 2, 2,
                                   byref(h))
     assert rc == 7 and h.value == 5
+
+
+def test_knn_graph_argument_checks(ovvs):
+    """ovvsIvfPqKnnGraph (additive; the reference's CAGRA IVF-PQ initializer,
+    src/neighbors/graphs.cpp:767-797): null pointers and a negative degree are
+    INVALID_ARGUMENT, a degree past the shortlist limit DEVICE_UNAVAILABLE, the inner
+    build's checks pass through, and the graph is untouched on failure."""
+    lib = ovvs._lib
+    res = ovvs.Resources()
+    x = np.zeros((8, 4), dtype=np.float32)
+    xp = x.ctypes.data_as(POINTER(c_float))
+    g = np.full(64, 7, dtype=np.int32)
+    gp = g.ctypes.data_as(POINTER(c_int32))
+    assert lib.ovvsIvfPqKnnGraph(None, xp, 8, 4, 0, 4, gp) == 2
+    assert lib.ovvsIvfPqKnnGraph(res._h, None, 8, 4, 0, 4, gp) == 2
+    assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 0, 4, None) == 2
+    assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 0, -1, gp) == 2
+    assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 0, 1024, gp) == 7
+    assert lib.ovvsIvfPqKnnGraph(res._h, xp, 0, 4, 0, 4, gp) == 2     # the build's n check
+    assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 9, 4, gp) == 2     # the build's metric check
+    assert np.all(g == 7)
+    if not res.gpu_available():
+        assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 0, 4, gp) == 7
+        assert np.all(g == 7)
