@@ -14,6 +14,7 @@
 #include "status.h"
 #include "version.h"
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -150,10 +151,13 @@ OVVS_API ovvsStatus ovvsIvfPqExtend(ovvsResources_t res, ovvsIvfPqIndex_t index,
 OVVS_API ovvsStatus ovvsIvfPqDestroy(ovvsIvfPqIndex_t index);
 
 /* ADDITIVE (no reference counterpart; the reference builds fp32 tables only).
- * ovvsIvfPqSearch with a choice of lookup-table precision: lut_dtype is
- * OVVS_DTYPE_F32 (identical to ovvsIvfPqSearch) or OVVS_DTYPE_F16 (each fp32
- * table entry rounded to binary16, round-to-nearest-even, overflow to +inf;
- * sums stay fp32). Any other dtype returns OVVS_STATUS_UNSUPPORTED. */
+ * ovvsIvfPqSearch with a requested lookup-table precision: lut_dtype is
+ * OVVS_DTYPE_F32 or OVVS_DTYPE_F16; any other dtype returns
+ * OVVS_STATUS_UNSUPPORTED. The scan computes each table entry in registers where
+ * a row uses it and stores no table, so binary16 entries would save neither
+ * memory traffic nor storage; both precisions are served with fp32 entries and
+ * return exactly the results of ovvsIvfPqSearch (no entry can overflow a
+ * binary16 range, and ovvsResourcesLastComputeDtype reports OVVS_DTYPE_F32). */
 OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t index,
                                       const float* queries, int64_t nq, int64_t k,
                                       int32_t nprobe, int32_t krefine, const uint8_t* bitset,

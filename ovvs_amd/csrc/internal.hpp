@@ -128,6 +128,22 @@ void saturating_add(int64_t& value, int64_t delta) noexcept;
 // there is none).
 bool gpu_present();
 
+// Copies bytes from src to dst (host memory) with a small pool of worker threads
+// shared by the library (one copy at a time; a copy that finds the pool busy, or
+// that is too small to split, runs on the calling thread).
+void parallel_copy(void* dst, const void* src, size_t bytes);
+
+// ovvsIvfPqSearchDevice with every workspace buffer carved from the caller's
+// scratch (device memory of scratch_bytes bytes) instead of the Resources'
+// workspace: no device or host memory is allocated. The index must already be
+// resident on the device (INVALID_ARGUMENT otherwise); a batch whose buffers do
+// not fit the scratch returns SHAPE_MISMATCH.
+ovvsStatus ivf_pq_search_scratch(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                 const float* queries, int64_t nq, int64_t k, int32_t nprobe,
+                                 int32_t krefine, const uint8_t* bitset, ovvsDType lut_dtype,
+                                 int64_t* neighbors, float* distances, void* scratch,
+                                 size_t scratch_bytes);
+
 // Maps a HIP error to the ABI status.
 ovvsStatus status_from_hip(hipError_t e);
 

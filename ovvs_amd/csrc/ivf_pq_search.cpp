@@ -81,10 +81,17 @@ struct Carver {
     if (st_ != OVVS_STATUS_SUCCESS) return st_; \
   } while (0)
 
+// Where the caller's buffers live and where the workspace comes from.
+enum class Io {
+  kHost,     // host queries, bitset and outputs; the Resources' workspace
+  kDevice,   // device buffers; the Resources' workspace
+  kScratch,  // device buffers; the caller's scratch, nothing allocated
+};
+
 ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float* queries,
                        int64_t nq, int64_t k, int32_t nprobe, int32_t krefine,
-                       const uint8_t* bitset, ovvsDType lut_dtype, bool device_io,
-                       int64_t* neighbors, float* distances) {
+                       const uint8_t* bitset, ovvsDType lut_dtype, Io io, void* scratch,
+                       size_t scratch_bytes, int64_t* neighbors, float* distances) {
   const auto started = Clock::now();
   if (!res || !index || !queries || !neighbors || !distances || nq <= 0 || k <= 0 ||
       k > std::numeric_limits<int32_t>::max()) {
@@ -108,15 +115,18 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
               static_cast<uint64_t>(ix.nlist)) {
     return OVVS_STATUS_INVALID_ARGUMENT;
   }
+  // Table precision: the scan stores no table (each entry is computed in registers
+  // where a row uses it), so a binary16 table would save no memory traffic or
+  // storage, only rank candidates differently from the reference. Both accepted
+  // precisions are served with fp32 entries, the reference's arithmetic.
   if (lut_dtype != OVVS_DTYPE_F32 && lut_dtype != OVVS_DTYPE_F16) return OVVS_STATUS_UNSUPPORTED;
   const int32_t P = std::max(1, std::min(nprobe, ix.nlist));
   const int32_t R = krefine < static_cast<int32_t>(k) ? static_cast<int32_t>(k) : krefine;
-  const int lut_f16 = lut_dtype == OVVS_DTYPE_F16 ? 1 : 0;
   // Fixed limits of the kernels: fail closed, as the reference's GPU route does
   // for krefine > 128 (indexes.cpp:576-584).
   // OVVS_HIP_MAX_REFINE bounds krefine and k.
   if (R > OVVS_HIP_MAX_REFINE || P > OVVS_HIP_MAX_PROBES ||
-      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), lut_f16, R, P) == 0 ||
+      ovvs_hip_scan_lds_bytes(ix.pq_m, ix.pq_ks, static_cast<int32_t>(ix.dim), R, P) == 0 ||
       nq > 0x7fffffff || ix.n > 0x7fffffff) {
     return OVVS_STATUS_DEVICE_UNAVAILABLE;
   }
@@ -125,36 +135,68 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     std::lock_guard<std::mutex> lock(res->call_mutex);
     SEARCH_TRY(res->ensure_gpu());
     GpuWork work;
-    SEARCH_TRY(ix.ensure_device(*res, work));
+    if (io == Io::kScratch) {
+      // Nothing may be allocated: the device mirror of the index must exist.
+      std::lock_guard<std::mutex> dev_lock(ix.device_mutex);
+      if (!ix.dev || ix.dev->device != res->device) return OVVS_STATUS_INVALID_ARGUMENT;
+    } else {
+      SEARCH_TRY(ix.ensure_device(*res, work));
+    }
     const ovvs::IndexDevice& dv = *ix.dev;
     hipStream_t s = res->stream;
     const int32_t dim = static_cast<int32_t>(ix.dim);
+    const bool device_io = io != Io::kHost;
 
-    // Query chunk for the coarse score matrix.
-    int64_t qc = static_cast<int64_t>(kScoreChunkBytes / (static_cast<size_t>(ix.nlist) * 4));
-    qc = std::max<int64_t>(1, std::min<int64_t>(qc, nq));
     const size_t nqk = static_cast<size_t>(nq) * static_cast<size_t>(k);
     const size_t bitset_bytes = static_cast<size_t>((ix.n + 7) / 8);
+    const size_t qbytes = static_cast<size_t>(nq) * dim * 4;
 
-    size_t need = 0;
-    need += device_io ? 0 : align256(static_cast<size_t>(nq) * dim * 4);  // queries
-    need += align256(static_cast<size_t>(nq) * 4);                        // query norms
-    need += align256(static_cast<size_t>(nq) * P * 4);                    // probes
-    need += align256(static_cast<size_t>(nq) * 4);                        // probe fallback flags
-    need += 2 * align256(static_cast<size_t>(nq) * 4);                    // scan query order, keys
-    need += align256(static_cast<size_t>(qc) * ix.nlist * 4);             // score chunk
-    need += align256(static_cast<size_t>(nq) * R * 8);                    // shortlist keys
-    need += align256(static_cast<size_t>(nq) * R * 4);                    // shortlist positions
-    need += align256(static_cast<size_t>(nq) * 4);                        // shortlist counts
-    need += align256(static_cast<size_t>(nq) * 16);                       // scan statistics
-    need += device_io ? 0 : align256(nqk * 8) + align256(nqk * 4);        // staged outputs
-    need += align256(4 * 8);                                              // counters
-    need += (!device_io && bitset) ? align256(bitset_bytes) : 0;
-    SEARCH_TRY(res->reserve_workspace(need, work));
-    const size_t pinned_need = 4 * 8 + (device_io ? 0 : nqk * 12);
-    SEARCH_TRY(res->reserve_pinned(pinned_need));
+    // Every workspace buffer but the coarse score chunk.
+    size_t fixed = 0;
+    fixed += device_io ? 0 : align256(qbytes);                          // queries
+    fixed += align256(static_cast<size_t>(nq) * 4);                     // query norms
+    fixed += align256(static_cast<size_t>(nq) * P * 4);                 // probes
+    fixed += align256(static_cast<size_t>(nq) * 4);                     // probe fallback flags
+    fixed += 2 * align256(static_cast<size_t>(nq) * 4);                 // scan query order, keys
+    fixed += align256(static_cast<size_t>(nq) * R * 8);                 // shortlist keys
+    fixed += align256(static_cast<size_t>(nq) * R * 4);                 // shortlist positions
+    fixed += align256(static_cast<size_t>(nq) * 4);                     // shortlist counts
+    fixed += align256(static_cast<size_t>(nq) * 16);                    // scan statistics
+    fixed += device_io ? 0 : align256(nqk * 8) + align256(nqk * 4);     // staged outputs
+    fixed += align256(4 * 8);                                           // counters
+    fixed += (!device_io && bitset) ? align256(bitset_bytes) : 0;
+    // Query chunk of the coarse score matrix (the exact route and the probe's
+    // fallback work through it chunk by chunk).
+    const size_t row_bytes = static_cast<size_t>(ix.nlist) * 4;
+    int64_t qc = static_cast<int64_t>(kScoreChunkBytes / row_bytes);
+    unsigned char* base = nullptr;
+    if (io == Io::kScratch) {
+      if (fixed > scratch_bytes || (scratch_bytes - fixed) / row_bytes < 1 ||
+          reinterpret_cast<uintptr_t>(scratch) % 256 != 0) {
+        return OVVS_STATUS_SHAPE_MISMATCH;
+      }
+      qc = std::min<int64_t>(qc, static_cast<int64_t>(((scratch_bytes - fixed) & ~size_t(255)) / row_bytes));
+      qc = std::max<int64_t>(1, std::min<int64_t>(qc, nq));
+      base = static_cast<unsigned char*>(scratch);
+    } else {
+      qc = std::max<int64_t>(1, std::min<int64_t>(qc, nq));
+      SEARCH_TRY(res->reserve_workspace(fixed + align256(static_cast<size_t>(qc) * row_bytes), work));
+      base = static_cast<unsigned char*>(res->workspace.get());
+    }
+    // Pinned host staging: [counters 32 B | ids | distances | queries | bitset] with
+    // host buffers, the counters alone with device buffers, none with the scratch.
+    const size_t pin_ids = 256, pin_dist = pin_ids + align256(nqk * 8);
+    const size_t pin_q = pin_dist + align256(nqk * 4), pin_bits = pin_q + align256(qbytes);
+    if (io == Io::kHost) {
+      SEARCH_TRY(res->reserve_pinned(pin_bits + (bitset ? bitset_bytes : 0)));
+    } else if (io == Io::kDevice) {
+      SEARCH_TRY(res->reserve_pinned(32));
+    }
+    unsigned long long scratch_counters[4] = {0, 0, 0, 0};
+    unsigned char* pin = io == Io::kScratch ? reinterpret_cast<unsigned char*>(scratch_counters)
+                                            : static_cast<unsigned char*>(res->pinned);
 
-    Carver cv{static_cast<unsigned char*>(res->workspace.get())};
+    Carver cv{base};
     const float* d_q = device_io ? queries : nullptr;
     if (!device_io) d_q = cv.take<float>(static_cast<size_t>(nq) * dim);
     float* d_qn = cv.take<float>(static_cast<size_t>(nq));
@@ -162,7 +204,6 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     int32_t* d_flags = cv.take<int32_t>(static_cast<size_t>(nq));
     int32_t* d_order = cv.take<int32_t>(static_cast<size_t>(nq));
     int32_t* d_okeys = cv.take<int32_t>(static_cast<size_t>(nq));
-    float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
     uint64_t* d_skeys = cv.take<uint64_t>(static_cast<size_t>(nq) * R);
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
     int32_t* d_scnt = cv.take<int32_t>(static_cast<size_t>(nq));
@@ -173,18 +214,29 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     float* d_odist = device_io ? distances : cv.take<float>(nqk);
     unsigned long long* d_counters = cv.take<unsigned long long>(4);
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
-    if (!device_io && bitset) {
-      uint8_t* b = cv.take<uint8_t>(bitset_bytes);
-      SEARCH_HIP(hipMemcpyAsync(b, bitset, bitset_bytes, hipMemcpyHostToDevice, s));
-      ovvs::saturating_add(work.h2d_calls, 1);
-      ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(bitset_bytes));
-      d_bitset = b;
-    }
+    if (!device_io && bitset) d_bitset = cv.take<uint8_t>(bitset_bytes);
+    float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
+
     if (!device_io) {
-      const size_t qb = static_cast<size_t>(nq) * dim * 4;
-      SEARCH_HIP(hipMemcpyAsync(const_cast<float*>(d_q), queries, qb, hipMemcpyHostToDevice, s));
-      ovvs::saturating_add(work.h2d_calls, 1);
-      ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(qb));
+      // Host inputs go through the pinned staging buffer in pieces, so that the
+      // DMA of one piece overlaps the host copy of the next.
+      if (bitset) {
+        ovvs::parallel_copy(pin + pin_bits, bitset, bitset_bytes);
+        SEARCH_HIP(hipMemcpyAsync(const_cast<uint8_t*>(d_bitset), pin + pin_bits, bitset_bytes,
+                                  hipMemcpyHostToDevice, s));
+        ovvs::saturating_add(work.h2d_calls, 1);
+        ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(bitset_bytes));
+      }
+      constexpr size_t kPiece = size_t(1) << 20;
+      const unsigned char* src = reinterpret_cast<const unsigned char*>(queries);
+      unsigned char* dst = reinterpret_cast<unsigned char*>(const_cast<float*>(d_q));
+      for (size_t off = 0; off < qbytes; off += kPiece) {
+        const size_t len = std::min(kPiece, qbytes - off);
+        ovvs::parallel_copy(pin + pin_q + off, src + off, len);
+        SEARCH_HIP(hipMemcpyAsync(dst + off, pin + pin_q + off, len, hipMemcpyHostToDevice, s));
+        ovvs::saturating_add(work.h2d_calls, 1);
+      }
+      ovvs::saturating_add(work.h2d_bytes, static_cast<int64_t>(qbytes));
     }
     const bool mfma_probe =
         dv.cmfma.get() != nullptr && ovvs_hip_probe_mfma_supported(dim, ix.nlist, P) != 0;
@@ -274,7 +326,6 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.rord = dv.rord.as<int32_t>();
     sa.bitset = d_bitset;
     sa.K = R;
-    sa.lut_f16 = lut_f16;
     sa.out_keys = d_skeys;
     sa.out_pos = d_spos;
     sa.out_count = d_scnt;
@@ -306,13 +357,12 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     SEARCH_HIP(hipEventRecord(ev[4], s));
     work.kernel_launches += mfma_probe ? 3 + chunks : 5 + 2 * chunks;
 
-    unsigned char* pin = static_cast<unsigned char*>(res->pinned);
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));
     ovvs::saturating_add(work.d2h_calls, 1);
     ovvs::saturating_add(work.d2h_bytes, 32);
     if (!device_io) {
-      SEARCH_HIP(hipMemcpyAsync(pin + 32, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
-      SEARCH_HIP(hipMemcpyAsync(pin + 32 + nqk * 8, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));
+      SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
+      SEARCH_HIP(hipMemcpyAsync(pin + pin_dist, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));
       ovvs::saturating_add(work.d2h_calls, 2);
       ovvs::saturating_add(work.d2h_bytes, static_cast<int64_t>(nqk * 12));
     }
@@ -326,8 +376,8 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
 
     // Success: publish the host outputs (device outputs already hold the results).
     if (!device_io) {
-      std::memcpy(neighbors, pin + 32, nqk * 8);
-      std::memcpy(distances, pin + 32 + nqk * 8, nqk * 4);
+      ovvs::parallel_copy(neighbors, pin + pin_ids, nqk * 8);
+      ovvs::parallel_copy(distances, pin + pin_dist, nqk * 4);
     }
 
     ovvsIvfPqSearchStatsV1 d{};
@@ -370,7 +420,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       for (int i = 0; i < 24; ++i) ovvs::saturating_add(dst[i], src[i]);
     }
     res->last_device = OVVS_DEVICE_GPU;
-    res->last_compute_dtype = lut_f16 ? OVVS_DTYPE_F16 : OVVS_DTYPE_F32;
+    res->last_compute_dtype = OVVS_DTYPE_F32;
     return OVVS_STATUS_SUCCESS;
   } catch (const std::bad_alloc&) {
     return OVVS_STATUS_OOM;
@@ -381,14 +431,24 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
 
 }  // namespace
 
+ovvsStatus ovvs::ivf_pq_search_scratch(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                       const float* queries, int64_t nq, int64_t k,
+                                       int32_t nprobe, int32_t krefine, const uint8_t* bitset,
+                                       ovvsDType lut_dtype, int64_t* neighbors, float* distances,
+                                       void* scratch, size_t scratch_bytes) {
+  if (!scratch) return OVVS_STATUS_INVALID_ARGUMENT;
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, Io::kScratch,
+                     scratch, scratch_bytes, neighbors, distances);
+}
+
 extern "C" {
 
 OVVS_API ovvsStatus ovvsIvfPqSearch(ovvsResources_t res, ovvsIvfPqIndex_t index,
                                     const float* queries, int64_t nq, int64_t k, int32_t nprobe,
                                     int32_t krefine, const uint8_t* bitset, int64_t* neighbors,
                                     float* distances) {
-  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, OVVS_DTYPE_F32, false,
-                     neighbors, distances);
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, OVVS_DTYPE_F32, Io::kHost,
+                     nullptr, 0, neighbors, distances);
 }
 
 OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t index,
@@ -396,8 +456,8 @@ OVVS_API ovvsStatus ovvsIvfPqSearchEx(ovvsResources_t res, ovvsIvfPqIndex_t inde
                                       int32_t nprobe, int32_t krefine, const uint8_t* bitset,
                                       ovvsDType lut_dtype, int64_t* neighbors,
                                       float* distances) {
-  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, false,
-                     neighbors, distances);
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, Io::kHost,
+                     nullptr, 0, neighbors, distances);
 }
 
 OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t index,
@@ -405,8 +465,8 @@ OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t 
                                           int32_t nprobe, int32_t krefine,
                                           const uint8_t* bitset, ovvsDType lut_dtype,
                                           int64_t* neighbors, float* distances) {
-  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, true,
-                     neighbors, distances);
+  return search_impl(res, index, queries, nq, k, nprobe, krefine, bitset, lut_dtype, Io::kDevice,
+                     nullptr, 0, neighbors, distances);
 }
 
 }  // extern "C"

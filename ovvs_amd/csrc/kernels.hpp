@@ -151,7 +151,6 @@ struct OvvsScanArgs {
   const int32_t* rord;         // [positions] index of each row within its list
   const uint8_t* bitset;       // (n+7)/8 bytes or nullptr
   int32_t K;                   // shortlist length (krefine), 1..OVVS_HIP_MAX_REFINE
-  int32_t lut_f16;             // 0: fp32 table entries, 1: binary16 entries
   uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
   int32_t* out_pos;            // [nq * K] scan positions
   int32_t* out_count;          // [nq]
@@ -174,7 +173,7 @@ hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, co
 int32_t ovvs_hip_query_key_shift(int32_t nlist);
 // Dynamic LDS bytes the scan kernel needs for these shapes, shortlist length and
 // probe count (0 if they exceed the 160 KiB a gfx950 workgroup can hold).
-size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t lut_f16, int32_t K,
+size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t K,
                                int32_t P);
 
 struct OvvsRefineArgs {

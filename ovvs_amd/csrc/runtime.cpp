@@ -8,10 +8,15 @@
 // staging, timing events and the IVF-PQ telemetry.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <new>
+#include <thread>
 
 #include "internal.hpp"
 
@@ -49,6 +54,124 @@ bool gpu_present() {
     return hipGetDeviceCount(&count) == hipSuccess && count > 0;
   }();
   return present;
+}
+
+namespace {
+
+// Worker threads that split host copies between them. A copy is cut into parts;
+// the caller and the workers claim parts from one counter that also carries the
+// copy's sequence number, so a worker that wakes late cannot claim a part of a
+// copy that has already finished.
+class CopyPool {
+ public:
+  static CopyPool& instance() {
+    // Never destroyed: its detached workers may be blocked on the condition
+    // variable when the process exits.
+    static CopyPool* pool = new CopyPool();
+    return *pool;
+  }
+
+  void copy(void* dst, const void* src, size_t bytes) {
+    if (bytes < kMinSplit || workers_ == 0) {
+      std::memcpy(dst, src, bytes);
+      return;
+    }
+    std::unique_lock<std::mutex> one(busy_, std::try_to_lock);
+    if (!one.owns_lock()) {
+      std::memcpy(dst, src, bytes);
+      return;
+    }
+    const size_t parts = std::min<size_t>(4 * (workers_ + 1), (bytes + kMinPart - 1) / kMinPart);
+    {
+      std::lock_guard<std::mutex> lk(m_);
+      job_.dst = static_cast<unsigned char*>(dst);
+      job_.src = static_cast<const unsigned char*>(src);
+      job_.bytes = bytes;
+      job_.parts = static_cast<uint32_t>(parts);
+      job_.part = (bytes + parts - 1) / parts;
+      ++seq_;
+      job_.seq = seq_;
+      left_.store(static_cast<uint32_t>(parts));
+      next_.store(static_cast<uint64_t>(seq_) << 32);
+    }
+    wake_.notify_all();
+    Job mine;
+    {
+      std::lock_guard<std::mutex> lk(m_);
+      mine = job_;
+    }
+    run(mine);
+    std::unique_lock<std::mutex> lk(m_);
+    done_.wait(lk, [&] { return left_.load() == 0; });
+  }
+
+ private:
+  static constexpr size_t kMinSplit = size_t(256) << 10;
+  static constexpr size_t kMinPart = size_t(64) << 10;
+
+  struct Job {
+    unsigned char* dst = nullptr;
+    const unsigned char* src = nullptr;
+    size_t bytes = 0;
+    size_t part = 0;
+    uint32_t parts = 0;
+    uint32_t seq = 0;
+  };
+
+  CopyPool() {
+    const unsigned hw = std::thread::hardware_concurrency();
+    workers_ = hw > 1 ? std::min(6u, hw - 1) : 0u;
+    for (unsigned i = 0; i < workers_; ++i) std::thread([this] { loop(); }).detach();
+  }
+
+  void loop() {
+    uint32_t seen = 0;
+    for (;;) {
+      Job j;
+      {
+        std::unique_lock<std::mutex> lk(m_);
+        wake_.wait(lk, [&] { return seq_ != seen; });
+        seen = seq_;
+        j = job_;
+      }
+      run(j);
+    }
+  }
+
+  // Claims and copies parts of copy j until none is left (or j has ended).
+  void run(const Job& j) {
+    for (;;) {
+      uint64_t v = next_.load();
+      uint32_t i;
+      do {
+        if (static_cast<uint32_t>(v >> 32) != j.seq) return;
+        i = static_cast<uint32_t>(v);
+        if (i >= j.parts) return;
+      } while (!next_.compare_exchange_weak(v, v + 1));
+      const size_t off = static_cast<size_t>(i) * j.part;
+      if (off < j.bytes) std::memcpy(j.dst + off, j.src + off, std::min(j.part, j.bytes - off));
+      if (left_.fetch_sub(1) == 1) {
+        std::lock_guard<std::mutex> lk(m_);
+        done_.notify_all();
+      }
+    }
+  }
+
+  unsigned workers_ = 0;
+  std::mutex busy_;  // one copy at a time
+  std::mutex m_;
+  std::condition_variable wake_, done_;
+  Job job_;
+  uint32_t seq_ = 0;
+  std::atomic<uint64_t> next_{0};  // sequence << 32 | next part
+  std::atomic<uint32_t> left_{0};  // parts not yet copied
+};
+
+}  // namespace
+
+void parallel_copy(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return;
+  CopyPool::instance().copy(dst, src, bytes);
 }
 
 ovvsStatus status_from_hip(hipError_t e) {

@@ -253,13 +253,13 @@ struct Codeword {
 
 // Table slice builders for the first phase (whole lists, all four waves): entry
 // (m - m0) * ks + j of the slice is sum_u (r[m*dsub+u] - B[m][j][u])^2, left to
-// right from +0 (binary16-rounded for F16 tables). For ks = 256 thread j computes
+// right from +0. For ks = 256 thread j computes
 // entry j of every subspace of the slice, its codebook loads (coalesced across
 // threads) issued a group of subspaces ahead of the arithmetic.
-template <int DSUB, bool F16>
+template <int DSUB>
 __device__ __forceinline__ void build_slice_256(const float* resid,
                                                 const float* __restrict__ codebooks, int m0,
-                                                float* lut32, uint16_t* lut16) {
+                                                float* lut32) {
   constexpr int kGroup = DSUB <= 2 ? kBlock : 16 / DSUB;
   const int j = static_cast<int>(threadIdx.x);
   const float* __restrict__ cb = codebooks + (static_cast<int64_t>(m0) * 256 + j) * DSUB;
@@ -277,20 +277,15 @@ __device__ __forceinline__ void build_slice_256(const float* resid,
         const float t = r[u] - cw[i].v[u];
         acc = acc + t * t;
       }
-      if (F16) {
-        lut16[(g0 + i) * 256 + j] = __half_as_ushort(__float2half_rn(acc));
-      } else {
-        lut32[(g0 + i) * 256 + j] = acc;
-      }
+      lut32[(g0 + i) * 256 + j] = acc;
     }
   }
 }
 
 // Any shape: mb subspaces of ks entries, dsub dimensions each.
-template <bool F16>
 __device__ __forceinline__ void build_slice_any(const float* resid, const float* __restrict__ codebooks,
                                                 int m0, int mb, int ks, int ks_log2, int dsub,
-                                                float* lut32, uint16_t* lut16) {
+                                                float* lut32) {
   const int slice = mb << ks_log2;
   for (int e = static_cast<int>(threadIdx.x); e < slice; e += kThreads) {
     const int m = m0 + (e >> ks_log2);
@@ -301,18 +296,14 @@ __device__ __forceinline__ void build_slice_any(const float* resid, const float*
       const float t = r[u] - cw[u];
       acc = acc + t * t;
     }
-    if (F16) {
-      lut16[e] = __half_as_ushort(__float2half_rn(acc));
-    } else {
-      lut32[e] = acc;
-    }
+    lut32[e] = acc;
   }
 }
 
 // One table entry computed directly from the codebook, with the operation order
 // of the reference's table build: sum_u (r[m*dsub+u] - B[m][code][u])^2 left to
-// right from +0 (binary16-rounded for F16 tables).
-template <int FD, bool F16>
+// right from +0.
+template <int FD>
 __device__ __forceinline__ float direct_entry(const float* resid, const float* __restrict__ codebooks,
                                               int m, int code, int ks, int dsub) {
   const int d = FD > 0 ? FD : dsub;
@@ -333,7 +324,6 @@ __device__ __forceinline__ float direct_entry(const float* resid, const float* _
       acc = acc + t * t;
     }
   }
-  if (F16) acc = __half2float(__float2half_rn(acc));
   return acc;
 }
 
@@ -470,7 +460,7 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
 
 // FD > 0: the shape-specialised body for ks = 256, pq_m % 8 == 0 and dsub = FD;
 // FD = 0: any shape.
-template <int KPL, bool F16, int FD>
+template <int KPL, int FD>
 __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char* smem) {
   const ScanLayout L = scan_layout(a.dim, KPL, a.P);
   const int dim_pad = (a.dim + 3) & ~3;
@@ -717,14 +707,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 #pragma unroll
           for (int j = 0; j < kBlock; ++j) {
             const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
-            v[j] = direct_entry<FD, F16>(resid, a.codebooks, m0 + j, code, ks, dsub);
+            v[j] = direct_entry<FD>(resid, a.codebooks, m0 + j, code, ks, dsub);
           }
 #pragma unroll
           for (int j = 0; j < kBlock; ++j) sc = sc + v[j];
         } else {
           for (int j = 0; j < mb; ++j) {
             const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
-            sc = sc + direct_entry<FD, F16>(resid, a.codebooks, m0 + j, code, ks, dsub);
+            sc = sc + direct_entry<FD>(resid, a.codebooks, m0 + j, code, ks, dsub);
           }
         }
       }
@@ -825,7 +815,6 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
                     static_cast<size_t>(kWaves) * (kBufCap * 12 + kQueueCap * 8),
                 "table slice must fit the candidate buffers and survivor queues");
   float* lut32 = reinterpret_cast<float*>(smem + L.bufk_off);
-  uint16_t* lut16 = reinterpret_cast<uint16_t*>(smem + L.bufk_off);
   const int ks_log2 = __ffs(ks) - 1;
   // Candidates: the first kP0Cand groups of ranks 0 .. kWaves-1 (wave w evaluates
   // rank w's) with their bounds, as keys (bound key << 32 | w * kP0Cand + j).
@@ -909,9 +898,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
         __syncthreads();  // every wave is done with the previous slice (or buffers)
         if (FD > 0) {
-          build_slice_256<(FD > 0 ? FD : 1), F16>(resid, a.codebooks, m0, lut32, lut16);
+          build_slice_256<(FD > 0 ? FD : 1)>(resid, a.codebooks, m0, lut32);
         } else {
-          build_slice_any<F16>(resid, a.codebooks, m0, mb, ks, ks_log2, dsub, lut32, lut16);
+          build_slice_any(resid, a.codebooks, m0, mb, ks, ks_log2, dsub, lut32);
         }
         __syncthreads();
 #pragma unroll
@@ -925,7 +914,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 #pragma unroll
             for (int jj = 0; jj < kBlock; ++jj) {
               const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
-              v[jj] = F16 ? __half2float(__ushort_as_half(lut16[jj * 256 + code])) : lut32[jj * 256 + code];
+              v[jj] = lut32[jj * 256 + code];
             }
 #pragma unroll
             for (int jj = 0; jj < kBlock; ++jj) acc = acc + v[jj];
@@ -933,7 +922,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
             for (int jj = 0; jj < mb; ++jj) {
               const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
               const int idx = (jj << ks_log2) + code;
-              acc = acc + (F16 ? __half2float(__ushort_as_half(lut16[idx])) : lut32[idx]);
+              acc = acc + lut32[idx];
             }
           }
           sc[i] = acc;
@@ -1136,14 +1125,14 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 #pragma unroll
             for (int jj = 0; jj < kBlock; ++jj) {
               const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
-              v[jj] = direct_entry<FD, F16>(resid, a.codebooks, jj, code, ks, dsub);
+              v[jj] = direct_entry<FD>(resid, a.codebooks, jj, code, ks, dsub);
             }
 #pragma unroll
             for (int jj = 0; jj < kBlock; ++jj) sc = sc + v[jj];
           } else {
             for (int jj = 0; jj < mb0; ++jj) {
               const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
-              sc = sc + direct_entry<FD, F16>(resid, a.codebooks, jj, code, ks, dsub);
+              sc = sc + direct_entry<FD>(resid, a.codebooks, jj, code, ks, dsub);
             }
           }
           if (nblocks == 1) {
@@ -1226,33 +1215,33 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
 // latency-bound, and measured on C2 this balances occupancy against register
 // spills better than 8 (64 VGPRs) or 6 (80). Longer register lists keep the
 // compiler's own allocation.
-template <int KPL, bool F16, int FD>
+template <int KPL, int FD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  scan_query<KPL, F16, FD>(a, smem);
+  scan_query<KPL, FD>(a, smem);
 }
 
-template <int KPL, bool F16>
+template <int KPL>
 __global__ __launch_bounds__(kThreads) void k_scan_long(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  scan_query<KPL, F16, 0>(a, smem);
+  scan_query<KPL, 0>(a, smem);
 }
 
-template <int KPL, bool F16>
+template <int KPL>
 hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   void (*fn)(OvvsScanArgs);
   if constexpr (KPL <= 2) {
     const bool shaped = a.ks == 256 && a.pq_m % kBlock == 0;
     switch (shaped ? a.dsub : 0) {
-      case 1: fn = k_scan<KPL, F16, 1>; break;
-      case 2: fn = k_scan<KPL, F16, 2>; break;
-      case 4: fn = k_scan<KPL, F16, 4>; break;
-      case 8: fn = k_scan<KPL, F16, 8>; break;
-      default: fn = k_scan<KPL, F16, 0>;
+      case 1: fn = k_scan<KPL, 1>; break;
+      case 2: fn = k_scan<KPL, 2>; break;
+      case 4: fn = k_scan<KPL, 4>; break;
+      case 8: fn = k_scan<KPL, 8>; break;
+      default: fn = k_scan<KPL, 0>;
     }
   } else {
-    fn = k_scan_long<KPL, F16>;
+    fn = k_scan_long<KPL>;
   }
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -1268,12 +1257,11 @@ int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512
 
 }  // namespace
 
-extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim,
-                                          int32_t lut_f16, int32_t K, int32_t P) {
+extern "C" size_t ovvs_hip_scan_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t K,
+                                          int32_t P) {
   if (pq_m <= 0 || ks <= 0 || dim <= 0 || K <= 0 || K > OVVS_HIP_MAX_REFINE || P <= 0 ||
       P > OVVS_HIP_MAX_PROBES)
     return 0;
-  (void)lut_f16;
   const size_t b = scan_layout(dim, kpl_for(K), P).total;
   return b <= 160u * 1024u ? b : 0;
 }
@@ -1297,21 +1285,12 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
   if (a.P > OVVS_HIP_MAX_PROBES) return hipErrorInvalidValue;
   const size_t lds = scan_layout(a.dim, kpl, a.P).total;
   if (lds > 160u * 1024u) return hipErrorInvalidValue;
-  if (a.lut_f16) {
-    switch (kpl) {
-      case 1: return launch_scan<1, true>(a, lds, stream);
-      case 2: return launch_scan<2, true>(a, lds, stream);
-      case 4: return launch_scan<4, true>(a, lds, stream);
-      case 8: return launch_scan<8, true>(a, lds, stream);
-      default: return launch_scan<16, true>(a, lds, stream);
-    }
-  }
   switch (kpl) {
-    case 1: return launch_scan<1, false>(a, lds, stream);
-    case 2: return launch_scan<2, false>(a, lds, stream);
-    case 4: return launch_scan<4, false>(a, lds, stream);
-    case 8: return launch_scan<8, false>(a, lds, stream);
-    default: return launch_scan<16, false>(a, lds, stream);
+    case 1: return launch_scan<1>(a, lds, stream);
+    case 2: return launch_scan<2>(a, lds, stream);
+    case 4: return launch_scan<4>(a, lds, stream);
+    case 8: return launch_scan<8>(a, lds, stream);
+    default: return launch_scan<16>(a, lds, stream);
   }
 }
 

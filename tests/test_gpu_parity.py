@@ -1,9 +1,10 @@
 """GPU parity: libovvs on the MI355X against the reference and the oracle.
 
 Bar (north star): neighbor ids identical to the reference's, distances within
-1e-4 relative for fp32 tables (2e-3 for binary16 tables); every comparison here
-also checks that the fp32 path is bit-identical, which is what the kernels are
-built for (separately rounded fp32 in the reference's order).
+1e-4 relative for fp32 tables (2e-3 for binary16 table requests, which are
+served with fp32 entries); every comparison here also checks that the results
+are bit-identical, which is what the kernels are built for (separately rounded
+fp32 in the reference's order).
 """
 
 from __future__ import annotations
@@ -97,11 +98,14 @@ def test_gpu_build_matches_reference_build_bytes(ovvs, res, ref_cases, tmp_path)
         ix.close()
 
 
-def test_fp16_tables_match_oracle_extension(ovvs, res, ref_cases, tmp_path):
+def test_fp16_requests_return_the_reference_results(ovvs, res, ref_cases, tmp_path):
+    """A binary16 table request is served with fp32 entries: the results are the
+    reference's own, bit for bit (the scan stores no table, so binary16 entries
+    would only change the ranking)."""
     manifest, arrays = ref_cases
     for name in ("mid8", "mid4", "metric0", "metric2", "filters"):
         case = next(c for c in manifest if c["name"] == name)
-        say("fp16", name)
+        say("fp16 request", name)
         path = write_case_ipq1(case, arrays, tmp_path)
         orc = Oracle(read_ipq1(path))
         ix = ovvs.neighbors.ivf_pq.load(path, resources=res)
@@ -110,11 +114,48 @@ def test_fp16_tables_match_oracle_extension(ovvs, res, ref_cases, tmp_path):
             bits = arrays.get(f"{name}/s{j}/bitset")
             ids, d = ix.search_ex(q, s["k"], s["nprobe"], s["krefine"], bitset=bits,
                                   lut_dtype=ovvs.DTYPE_F16)
-            oids, od = orc.search(q, s["k"], s["nprobe"], s["krefine"], bits, lut_f16=True)
+            oids, od = orc.search(q, s["k"], s["nprobe"], s["krefine"], bits)
             assert_results_match(ids, d, oids, od, rel=2e-3, label=f"{name}/s{j}")
             assert_bits_unless_lp(case["metric"], d, od, f"{name}/s{j}")
+            assert np.array_equal(ids, arrays[f"{name}/s{j}/ids"]), f"{name}/s{j}"
         ix.close()
-    assert res.last_compute_dtype() == ovvs.DTYPE_F16
+    assert res.last_compute_dtype() == ovvs.DTYPE_F32
+
+
+def test_fp16_request_with_entries_beyond_binary16_range(ovvs, res, tmp_path):
+    """Data whose table entries exceed 65504, the largest binary16 value: a
+    binary16 table would hold +inf there. The search returns the reference's
+    fp32 results whatever precision is requested."""
+    rng = np.random.default_rng(31)
+    dim, n, nlist, pq_m = 16, 4000, 8, 8
+    centers = (400.0 * rng.standard_normal((8, dim))).astype(np.float32)
+    data = (centers[rng.integers(0, 8, n)] + 150.0 * rng.standard_normal((n, dim))).astype(
+        np.float32)
+    q = (centers[rng.integers(0, 8, 200)] + 150.0 * rng.standard_normal((200, dim))).astype(
+        np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=pq_m, pq_nbits=8, resources=res)
+    p = tmp_path / "wide.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    # The probed lists' tables do reach past the binary16 range.
+    probes = orc.probes(q[:20], 4)
+    big = max(float(orc.lut(q[i], int(probes[i, j])).max()) for i in range(20) for j in range(4))
+    say("largest table entry of the probed lists", big)
+    assert big > 65504.0
+    oids, od = orc.search(q, 10, 4, 32)
+    for dt in (ovvs.DTYPE_F32, ovvs.DTYPE_F16):
+        ids, d = ix.search_ex(q, 10, 4, 32, lut_dtype=dt)
+        assert np.array_equal(ids, oids), dt
+        assert np.array_equal(_bits(d), _bits(od)), dt
+    if REF_SO.exists():
+        ref = Reference()
+        rc, h = ref.load(p)
+        assert rc == 0
+        rc, rids, rd = ref.search(h, q, 10, 4, 32)
+        assert rc == 0 and np.array_equal(rids, oids) and np.array_equal(_bits(rd), _bits(od))
+        ref.destroy(h)
+        ref.close()
+    ix.close()
 
 
 def test_random_indexes_against_oracle(ovvs, res, tmp_path):
@@ -409,4 +450,61 @@ def test_c1_scale_against_reference(ovvs, res, tmp_path):
     assert np.array_equal(_bits(d), _bits(rd))
     ref.destroy(h)
     ref.close()
+    ix.close()
+
+
+def test_extend_is_transactional(ovvs, res, tmp_path):
+    """The reference's transactional-extend contract (reference
+    tests/test_neighbors.cpp:1427-1524, src/neighbors/indexes.cpp:1320-1427): a
+    failed extend leaves the serialized bytes and the search results unchanged;
+    after a successful one every extended row is its own nearest neighbour at
+    distance < 1e-5, and the extended index survives a reload byte for byte."""
+    from ovvs_amd.synth import lcg_data
+
+    n, dim, nq, k, nlist, pq_m = 64, 8, 4, 4, 8, 4
+    data = lcg_data(n, dim, 218)
+    extra = lcg_data(nq, dim, 219)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=pq_m, pq_nbits=4, resources=res)
+    base_ids, base_d = ix.search(data[:nq], k, nlist, n)
+    before = tmp_path / "before.ipq1"
+    ix.serialize(before)
+    before_bytes = before.read_bytes()
+
+    failing = extra.copy()
+    failing[0, 0] = np.nan
+    res.set_policy(ovvs.POLICY_FORCE_NPU)
+    try:
+        with pytest.raises(ovvs.OvvsError) as err:
+            ix.extend(failing)
+        assert err.value.status == ovvs.STATUS_DEVICE_UNAVAILABLE
+    finally:
+        res.set_policy(ovvs.POLICY_AUTO)
+    after = tmp_path / "after.ipq1"
+    ix.serialize(after)
+    assert after.read_bytes() == before_bytes, "failed extend changed the index"
+    ids, d = ix.search(data[:nq], k, nlist, n)
+    assert np.array_equal(ids, base_ids) and np.array_equal(_bits(d), _bits(base_d))
+
+    ix.extend(extra)
+    ext_ids, ext_d = ix.search(extra, 1, nlist, n + nq)
+    assert np.array_equal(ext_ids[:, 0], np.arange(n, n + nq)), ext_ids
+    assert np.all(np.abs(ext_d[:, 0]) < 1e-5), ext_d
+    ix.serialize(after)
+    re = ovvs.neighbors.ivf_pq.load(after, resources=res)
+    r_ids, r_d = re.search(extra, 1, nlist, n + nq)
+    assert np.array_equal(r_ids, ext_ids) and np.array_equal(_bits(r_d), _bits(ext_d))
+    again = tmp_path / "again.ipq1"
+    re.serialize(again)
+    assert again.read_bytes() == after.read_bytes(), "extended IPQ1 not byte stable"
+    if REF_SO.exists():
+        ref = Reference()
+        rc, h = ref.build(data, 0, nlist, pq_m, 4)
+        assert rc == 0
+        assert ref.extend(h, extra) == 0
+        ref_path = tmp_path / "ref.ipq1"
+        ref.save(h, ref_path)
+        assert ref_path.read_bytes() == after.read_bytes(), "extended bytes differ from the reference's"
+        ref.destroy(h)
+        ref.close()
+    re.close()
     ix.close()
