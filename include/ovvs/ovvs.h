@@ -179,6 +179,33 @@ OVVS_API ovvsStatus ovvsIvfPqSearchDevice(ovvsResources_t res, ovvsIvfPqIndex_t 
                                           const uint8_t* bitset, ovvsDType lut_dtype,
                                           int64_t* neighbors, float* distances);
 
+/* ADDITIVE — no counterpart in the reference. For callers that cannot allocate
+ * memory on the search path (code that must not call hipMalloc/hipFree or
+ * allocate pinned host memory: tight serving loops, harnesses that forbid
+ * allocation). Same arguments, semantics and results as ovvsIvfPqSearchDevice,
+ * but no device or host memory is allocated: the search's workspace is carved
+ * from a fixed device array of OVVS_NOALLOC_SCRATCH_BYTES that every GPU the
+ * library runs on holds until the process ends.
+ *   - The index must already have its device copy on this GPU: the first search
+ *     of an index through ovvsIvfPqSearch, ovvsIvfPqSearchEx or
+ *     ovvsIvfPqSearchDevice makes it (ovvsIvfPqExtend drops it again). Without it
+ *     the call returns OVVS_STATUS_INVALID_ARGUMENT.
+ *   - A batch whose workspace exceeds the array returns OVVS_STATUS_SHAPE_MISMATCH
+ *     with the outputs untouched. The workspace is about
+ *     nq * (40 + 4 * nprobe + 12 * max(k, krefine)) bytes plus one row of
+ *     4 * nlist bytes of coarse scores (C2's 10,000-query batch: 4.2 MB).
+ *   - Calls on one GPU share its array and run one at a time (the library
+ *     serializes them); the array keeps the last call's contents and the search
+ *     clears what it needs itself.
+ *   - The first call on a Resources opens its HIP stream, as any entry point
+ *     does. */
+#define OVVS_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+OVVS_API ovvsStatus ovvsIvfPqSearchDeviceNoAlloc(ovvsResources_t res, ovvsIvfPqIndex_t index,
+                                                 const float* queries, int64_t nq, int64_t k,
+                                                 int32_t nprobe, int32_t krefine,
+                                                 const uint8_t* bitset, ovvsDType lut_dtype,
+                                                 int64_t* neighbors, float* distances);
+
 /* ADDITIVE (the reference computes this inside its CAGRA build: the IVF-PQ
  * initializer, reference src/neighbors/graphs.cpp:767-797, with no entry point of its
  * own). The k-nearest-neighbour graph of the rows by IVF-PQ: an index is built with

@@ -56,6 +56,8 @@ METRIC_HAMMING = 4
 METRIC_LP = 5
 DTYPE_F32 = 0
 DTYPE_F16 = 1
+# Size of the device scratch ovvsIvfPqSearchDeviceNoAlloc carves its workspace from.
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 OVVS_IVF_PQ_SEARCH_STATS_ABI_V1 = 1
 _STATS_FIELDS = (
@@ -117,6 +119,8 @@ _SIGS = {
                                     c_int32, _V, c_int32, POINTER(c_int64), POINTER(c_float)]),
     "ovvsIvfPqSearchDevice": (c_int32, [_V, _V, _V, c_int64, c_int64, c_int32, c_int32, _V,
                                         c_int32, _V, _V]),
+    "ovvsIvfPqSearchDeviceNoAlloc": (c_int32, [_V, _V, _V, c_int64, c_int64, c_int32, c_int32,
+                                               _V, c_int32, _V, _V]),
     "ovvsIvfPqSerialize": (c_int32, [_V, c_char_p]),
     "ovvsIvfPqDeserialize": (c_int32, [_V, c_char_p, POINTER(_V)]),
     "ovvsIvfPqExtend": (c_int32, [_V, _V, POINTER(c_float), c_int64]),
@@ -300,6 +304,18 @@ class IvfPqIndex:
                                         c_int32(lut_dtype), c_void_p(ids_ptr),
                                         c_void_p(dists_ptr))
         _check_status(rc, "IVF-PQ device search")
+
+    def search_device_noalloc(self, queries_ptr: int, nq: int, k: int, nprobe: int,
+                              krefine: int, ids_ptr: int, dists_ptr: int,
+                              bitset_ptr: int | None = None, lut_dtype=DTYPE_F32) -> None:
+        """search_device without any allocation: the workspace is the library's fixed
+        device scratch (NOALLOC_SCRATCH_BYTES); the index must already be on the GPU."""
+        rc = _lib.ovvsIvfPqSearchDeviceNoAlloc(self._res._h, self._h, c_void_p(queries_ptr),
+                                               c_int64(nq), c_int64(k), c_int32(nprobe),
+                                               c_int32(krefine), c_void_p(bitset_ptr or 0),
+                                               c_int32(lut_dtype), c_void_p(ids_ptr),
+                                               c_void_p(dists_ptr))
+        _check_status(rc, "IVF-PQ no-allocation device search")
 
     def serialize(self, path) -> None:
         _check_status(_lib.ovvsIvfPqSerialize(self._h, str(path).encode()), "IVF-PQ serialize")
