@@ -10,10 +10,19 @@ n_probes=64, k=10, krefine=k, fp32 lookup tables, 10k-query batch.
 A step is one ovvsIvfPqSearchDevice call over the whole batch with queries and
 results already in HBM. value = queries / second over the timed steps.
 The JSON line also carries:
-  roofline      the code scan + select kernel: algorithmic code bytes per
-                launch (candidate_rows * pq_m from the library's telemetry)
-                divided by its average duration (HIP events on the library's
-                stream), against the 8 TB/s HBM peak;
+  roofline      the dominant kernel, the code scan + select (k_scan). It reads
+                only the code bytes of rows its lower bounds cannot rule out, so
+                its busiest resource is VALU issue, not HBM: achieved = its VALU
+                instructions per launch (rocprofv3 SQ_INSTS_VALU, committed under
+                profiles/) over its average duration measured here (HIP events on
+                the library's stream), against two wave64 VALU instructions per CU
+                per clock (the fp32 vector peak); beside it the HBM fraction of its
+                measured traffic and, labelled as such, the rate a full scan of the
+                same code bytes would need;
+  probe         the coarse probe on the matrix cores: the reference's GEMM flops
+                (2 nq nlist dim) and the bf16 flops executed, over its duration;
+  measured_peaks  streaming-read HBM GB/s, bf16 / fp32 MFMA TFLOP/s and VALU
+                issue, measured on this GPU by ovvs_amd/lib/libovvs_peaks.so;
   cpu_baseline  the reference library's own CPU search (oracle/_ref, built
                 from /root/reference) on the same index: the whole batch over
                 --cpu-threads threads (one Resources each, the reference's
@@ -21,7 +30,11 @@ The JSON line also carries:
                 --cpu-sample prefix (`value_1_thread`);
   parity_vs_reference  the whole batch, GPU fp32-table answers against the
                 reference's: identical rows, bit-identical distances;
-  recall_at_k   against exact brute force (fp32 on the GPU, torch matmul).
+  recall_at_k   against exact brute force (fp32 on the GPU, torch matmul);
+  host_io       the same batch through the host-pointer ABI (ovvsIvfPqSearch,
+                PCIe copies included), timed over the same number of steps;
+  krefine_32    QPS and recall with a re-rank shortlist of 32 (the reference
+                Python default) beside the configuration's krefine = k.
 Progress lines go to stderr; stdout carries exactly one JSON line.
 """
 
@@ -43,6 +56,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = ("IVF-PQ search QPS @k=10 (10k-query batch) at matched recall; "
           "scan HBM GB/s %peak")
 HBM_PEAK_GBS = 8000.0
+# MI355X: 256 CUs at 2.4 GHz; its 157.3 TFLOP/s fp32 vector peak (FMA = 2 flops) is
+# 128 lanes per CU per clock, two wave64 fp32 VALU instructions per CU per clock.
+VALU_PEAK_GINSTS = 157.3e3 / 2 / 64
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 T0 = time.time()
 
 
@@ -71,16 +89,50 @@ def exact_topk(base_t, q_t, k, torch):
     return best_i.cpu().numpy()
 
 
-def profiled_traffic(config_name):
-    """HBM bytes per k_scan launch from the committed rocprofv3 summary of this
-    workload (FETCH_SIZE and WRITE_SIZE passes, scaled by known-size copies)."""
-    path = ROOT / "profiles" / f"k_scan_{config_name}.md"
+def profile_value(profile, key):
+    """A `key: value` figure of a committed rocprofv3 summary (profiles/<profile>.md)
+    and the summary's path, or (None, None)."""
+    path = ROOT / "profiles" / f"{profile}.md"
     if not path.exists():
         return None, None
     for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(f"{key}:"):
             return float(line.split(":", 1)[1]), str(path.relative_to(ROOT))
     return None, None
+
+
+def measure_peaks(torch, dev):
+    """Ceilings measured on this GPU (ovvs_amd/lib/libovvs_peaks.so): a 4 GiB
+    streaming read (far beyond the 256 MB Infinity Cache), bf16 and fp32 MFMA and
+    VALU issue loops; best of five launches each."""
+    import ctypes
+
+    path = ROOT / "ovvs_amd" / "lib" / "libovvs_peaks.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    for fn in ("peaks_hbm_read", "peaks_mfma_bf16", "peaks_mfma_f32", "peaks_valu"):
+        getattr(lib, fn).restype = ctypes.c_double
+    lib.peaks_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
+    for fn in ("peaks_mfma_bf16", "peaks_mfma_f32", "peaks_valu"):
+        getattr(lib, fn).argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    scratch = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
+    buf = torch.ones(1 << 30, dtype=torch.float32, device=dev)  # 4 GiB
+    torch.cuda.synchronize()
+    out = {
+        "hbm_read_GBps": lib.peaks_hbm_read(buf.data_ptr(), buf.numel() * 4, scratch.data_ptr(), 5),
+        "mfma_bf16_TFLOPs": lib.peaks_mfma_bf16(scratch.data_ptr(), 4096, 5),
+        "mfma_f32_TFLOPs": lib.peaks_mfma_f32(scratch.data_ptr(), 4096, 5),
+        "valu_G_wave64_insts_per_s": lib.peaks_valu(scratch.data_ptr(), 16384, 5),
+    }
+    clock, cus = ctypes.c_int(0), ctypes.c_int(0)
+    lib.peaks_device_info.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    if lib.peaks_device_info(ctypes.byref(clock), ctypes.byref(cus)) == 0:
+        out["clock_MHz"] = clock.value
+        out["compute_units"] = cus.value
+    del buf, scratch
+    torch.cuda.synchronize()
+    return out
 
 
 def recall(got, truth):
@@ -244,6 +296,14 @@ def main() -> int:
                     help="processes generating the base rows of large configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak kernels")
+    ap.add_argument("--no-host-io", action="store_true",
+                    help="skip the host-pointer (PCIe-inclusive) timing")
+    ap.add_argument("--extra-krefine", type=int, default=32,
+                    help="also time and score this krefine (0: skip)")
+    ap.add_argument("--unclustered", action="store_true",
+                    help="isotropic N(0, I) rows and queries of the config's shape (no "
+                         "clusters: the scan's worst case)")
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
                     help="run one device-to-device copy and one elementwise copy of this many "
                          "MiB before the timed steps (known-size kernels that scale rocprofv3 "
@@ -260,11 +320,13 @@ def main() -> int:
     import ovvs_amd
     from ovvs_amd import synth
 
+    import dataclasses
+
     cfg = synth.CONFIGS[args.config]
     if args.rows:
-        import dataclasses
-
         cfg = dataclasses.replace(cfg, n=args.rows, train_rows=min(cfg.train_rows, args.rows))
+    if args.unclustered:
+        cfg = dataclasses.replace(cfg, kind="iso")
     nq = args.nq or cfg.nq
     k = cfg.k
     krefine = args.krefine or k
@@ -358,30 +420,105 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
     dsd = {key: s1[key] - s0[key] for key in s1 if isinstance(s1[key], int)}
     calls = dsd["successful_calls"]
     scan_s = dsd["adc_scan_select_ns"] / calls * 1e-9
+    probe_s = dsd["coarse_pairwise_ns"] / calls * 1e-9
     code_bytes = dsd["candidate_rows"] / calls * cfg.pq_m
-    achieved = code_bytes / scan_s / 1e9
     stage_ms = {name: dsd[f"{name}_ns"] / calls * 1e-6
                 for name in ("coarse_pairwise", "coarse_topk", "adc_scan_select",
                              "refine_distance", "total_wall")}
-
-    traffic, traffic_src = profiled_traffic(cfg.name)
     gpu_ids = did.cpu().numpy()
     gpu_d = dd.cpu().numpy()
 
-    # PCIe-inclusive rate through the host-pointer ABI (reported, never `value`).
-    t = time.perf_counter()
-    host_steps = 3
-    for _ in range(host_steps):
-        hids, hd = index.search_ex(queries, k, cfg.nprobe, krefine, lut_dtype=lut)
-    qps_host = nq * host_steps / (time.perf_counter() - t)
-    if not (np.array_equal(hids, gpu_ids) and np.array_equal(hd, gpu_d)):
-        raise AssertionError("host-pointer and device-pointer searches disagree")
+    # The host-pointer ABI over the same number of steps (PCIe copies of queries
+    # and results included; reported beside `value`, never as it).
+    host = None
+    if not args.no_host_io:
+        for _ in range(2):
+            hids, hd = index.search_ex(queries, k, cfg.nprobe, krefine, lut_dtype=lut)
+        t = time.perf_counter()
+        for _ in range(args.steps):
+            hids, hd = index.search_ex(queries, k, cfg.nprobe, krefine, lut_dtype=lut)
+        dt = time.perf_counter() - t
+        if not (np.array_equal(hids, gpu_ids) and np.array_equal(hd, gpu_d)):
+            raise AssertionError("host-pointer and device-pointer searches disagree")
+        host = {"queries_per_s": nq * args.steps / dt, "ms_per_step": dt * 1e3 / args.steps,
+                "steps": args.steps}
+        log(f"host-pointer ABI: {host['ms_per_step']:.3f} ms/step, {host['queries_per_s']:,.0f} QPS")
 
+    truth = None
     rec = None
     if not args.no_recall:
         truth = exact_topk(torch.from_numpy(base).to(dev), dq, k, torch)
         rec = recall(gpu_ids, truth)
         log(f"recall@{k} vs exact = {rec:.4f}")
+
+    extra = None
+    if args.extra_krefine and args.extra_krefine != krefine:
+        kr2 = max(args.extra_krefine, k)
+        for _ in range(2):
+            index.search_device(dq.data_ptr(), nq, k, cfg.nprobe, kr2, did.data_ptr(),
+                                dd.data_ptr(), lut_dtype=lut)
+        torch.cuda.synchronize()
+        steps2 = max(1, args.steps // 2)
+        t = time.perf_counter()
+        for _ in range(steps2):
+            index.search_device(dq.data_ptr(), nq, k, cfg.nprobe, kr2, did.data_ptr(),
+                                dd.data_ptr(), lut_dtype=lut)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        extra = {"krefine": kr2, "queries_per_s": nq * steps2 / dt,
+                 "ms_per_step": dt * 1e3 / steps2, "steps": steps2,
+                 "recall_at_k": recall(did.cpu().numpy(), truth) if truth is not None else None}
+        log(f"krefine {kr2}: {extra['ms_per_step']:.3f} ms/step, recall {extra['recall_at_k']}")
+
+    peaks = None if args.no_peaks else measure_peaks(torch, dev)
+    if peaks:
+        log("measured peaks: " + ", ".join(f"{a} {b:,.1f}" for a, b in peaks.items()))
+
+    # Roofline of the dominant kernel (the scan) from its committed counters.
+    prof = f"k_scan_{cfg.name}" + ("_unclustered" if args.unclustered else "")
+    valu, valu_src = profile_value(prof, "valu_insts_per_launch")
+    traffic, traffic_src = profile_value(prof, "traffic_bytes_per_launch")
+    roof = {
+        "kernel": "k_scan (segment-bounded code scan + shortlist)",
+        "bound": "valu",
+        "unit": "G wave64 VALU instructions/s",
+        "achieved": valu / scan_s / 1e9 if valu else None,
+        "peak": VALU_PEAK_GINSTS,
+        "frac": valu / scan_s / 1e9 / VALU_PEAK_GINSTS if valu else None,
+        "valu_insts_per_launch": valu,
+        "avg_launch_ms": scan_s * 1e3,
+        "traffic": traffic,
+        "hbm_GBps": traffic / scan_s / 1e9 if traffic else None,
+        "hbm_frac": traffic / scan_s / 1e9 / HBM_PEAK_GBS if traffic else None,
+        "counters_source": valu_src or traffic_src,
+        "algorithmic_equivalent": {
+            "note": "code bytes a full scan of every probed list reads (candidate_rows x "
+                    "pq_dim, each (query, list) pair counted); the scan reads only rows its "
+                    "lower bounds cannot rule out, so this rate is not an HBM figure",
+            "bytes_per_launch": code_bytes,
+            "GBps": code_bytes / scan_s / 1e9,
+        },
+    }
+    if peaks and roof["achieved"]:
+        roof["peak_measured"] = peaks["valu_G_wave64_insts_per_s"]
+        roof["frac_measured"] = roof["achieved"] / peaks["valu_G_wave64_insts_per_s"]
+    if peaks and roof["hbm_GBps"]:
+        roof["hbm_frac_measured"] = roof["hbm_GBps"] / peaks["hbm_read_GBps"]
+    gemm_flops = 2.0 * nq * cfg.nlist * cfg.dim
+    bf16_flops, bf16_src = profile_value(f"k_probe_mfma_{cfg.name}", "bf16_flops_per_launch")
+    probe = {
+        "kernel": "k_probe_mfma (coarse probe on the matrix cores, exact by proof)",
+        "bound": "mfma",
+        "avg_launch_ms": probe_s * 1e3,
+        "gemm_flops_per_launch": gemm_flops,
+        "achieved_TFLOPs": gemm_flops / probe_s / 1e12,
+        "frac_of_fp32_mfma_peak": gemm_flops / probe_s / 1e12 / MFMA_F32_PEAK_TFLOPS,
+        "bf16_flops_executed_per_launch": bf16_flops,
+        "bf16_TFLOPs": bf16_flops / probe_s / 1e12 if bf16_flops else None,
+        "frac_of_bf16_mfma_peak": bf16_flops / probe_s / 1e12 / MFMA_BF16_PEAK_TFLOPS
+        if bf16_flops else None,
+        "counters_source": bf16_src,
+    }
 
     cpu, parity = (None, None)
     if not args.no_cpu_baseline:
@@ -402,32 +539,27 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if cfg.lut_f16 else "f32",
+        "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"ivfpq_{cfg.name}_{cfg.n}x{cfg.dim}_nlist{cfg.nlist}_pq{cfg.pq_m}x8_"
+            "workload": f"ivfpq_{cfg.name}{'_unclustered' if args.unclustered else ''}_"
+                        f"{cfg.n}x{cfg.dim}_nlist{cfg.nlist}_pq{cfg.pq_m}x8_"
                         f"nprobe{cfg.nprobe}_k{k}_nq{nq}_{'f16' if cfg.lut_f16 else 'f32'}lut",
+            "lut_requested": "f16" if cfg.lut_f16 else "f32",
+            "lut_computed": "f32",
             "n": cfg.n, "dim": cfg.dim, "nlist": cfg.nlist, "pq_dim": cfg.pq_m, "pq_bits": 8,
             "n_probes": cfg.nprobe, "k": k, "krefine": krefine, "batch": nq,
             "train_rows": cfg.train_rows, "parallelism": "single-gpu",
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "traffic_source": traffic_src,
-            "kernel": "k_scan (segment-bounded code scan + shortlist)",
-            "algorithmic_bytes_per_launch": code_bytes,
-            "avg_launch_ms": scan_s * 1e3,
-        },
+        "roofline": roof,
+        "probe": probe,
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "stage_ms": stage_ms,
         "smaller_batches": small,
-        "qps_host_io": qps_host,
+        "host_io": host,
         "recall_at_k": rec,
+        "krefine_32": extra,
         "recall_k": k,
         "parity_vs_reference": parity,
     }

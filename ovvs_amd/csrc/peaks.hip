@@ -126,11 +126,13 @@ int cu_count() {
 
 }  // namespace
 
+#define PEAKS_API __attribute__((visibility("default")))
+
 extern "C" {
 
 // src: device buffer of `bytes` (a multiple of 16); scratch: device, one uint32 per
 // workgroup (gridDim <= 65536). Returns GB/s (1e9 bytes), 0 on error.
-double peaks_hbm_read(const void* src, size_t bytes, void* scratch, int reps) {
+PEAKS_API double peaks_hbm_read(const void* src, size_t bytes, void* scratch, int reps) {
   const int cus = cu_count();
   if (!src || !scratch || bytes < 16 || cus <= 0) return 0.0;
   const unsigned grid = static_cast<unsigned>(cus) * 16u;
@@ -143,7 +145,7 @@ double peaks_hbm_read(const void* src, size_t bytes, void* scratch, int reps) {
 }
 
 // scratch: device, one float per workgroup (8 workgroups of 4 waves per CU).
-double peaks_mfma_bf16(void* scratch, int iters, int reps) {
+PEAKS_API double peaks_mfma_bf16(void* scratch, int iters, int reps) {
   const int cus = cu_count();
   if (!scratch || iters <= 0 || cus <= 0) return 0.0;
   const unsigned grid = static_cast<unsigned>(cus) * 8u;
@@ -154,7 +156,7 @@ double peaks_mfma_bf16(void* scratch, int iters, int reps) {
   return ms > 0.0 ? flops / (ms * 1e-3) / 1e12 : 0.0;
 }
 
-double peaks_mfma_f32(void* scratch, int iters, int reps) {
+PEAKS_API double peaks_mfma_f32(void* scratch, int iters, int reps) {
   const int cus = cu_count();
   if (!scratch || iters <= 0 || cus <= 0) return 0.0;
   const unsigned grid = static_cast<unsigned>(cus) * 8u;
@@ -166,7 +168,7 @@ double peaks_mfma_f32(void* scratch, int iters, int reps) {
 }
 
 // Giga wave64 VALU instructions per second over the whole GPU.
-double peaks_valu(void* scratch, int iters, int reps) {
+PEAKS_API double peaks_valu(void* scratch, int iters, int reps) {
   const int cus = cu_count();
   if (!scratch || iters <= 0 || cus <= 0) return 0.0;
   const unsigned grid = static_cast<unsigned>(cus) * 8u;
@@ -178,7 +180,7 @@ double peaks_valu(void* scratch, int iters, int reps) {
 }
 
 // Shader clock (MHz) and compute units of the current device.
-int peaks_device_info(int* clock_mhz, int* cus) {
+PEAKS_API int peaks_device_info(int* clock_mhz, int* cus) {
   int dev = 0;
   if (!clock_mhz || !cus || hipGetDevice(&dev) != hipSuccess) return 1;
   int khz = 0;
