@@ -216,6 +216,74 @@ def cpu_baseline(index, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample, thr
     return base, parity
 
 
+def cpu_baseline_port(index, base, queries, gpu_ids, gpu_d, k, nprobe, krefine, sample, threads):
+    """Our C restatement of the reference CPU search (oracle/liboracle.so) on this host,
+    for indexes whose IPQ1 file the reference library would have to load from disk
+    (C5: 43 GB): the library serializes the index into a pipe, the reader keeps every
+    section but the dataset, and the bench's own rows stand in for it. Timed on the
+    first `sample` queries over `threads` threads (and a tenth of them on one thread);
+    parity is checked on the same queries."""
+    import threading
+
+    from oracle.pyoracle import ORACLE_SO, Oracle, read_ipq1_stream
+
+    if not ORACLE_SO.exists():
+        return None, None
+    log("cpu baseline (port): streaming the index out of the library")
+    with tempfile.TemporaryDirectory() as d:
+        fifo = Path(d) / "index.pipe"
+        os.mkfifo(fifo)
+        errs = []
+
+        def writer():
+            try:
+                index.serialize(fifo)
+            except Exception as e:  # noqa: BLE001 (reported after the join)
+                errs.append(e)
+
+        th = threading.Thread(target=writer)
+        th.start()
+        with open(fifo, "rb", buffering=1 << 20) as f:
+            try:
+                ipq = read_ipq1_stream(f, base)
+            except Exception:
+                while f.read(1 << 26):
+                    pass
+                th.join()
+                raise
+        th.join()
+        if errs:
+            raise errs[0]
+    orc = Oracle(ipq)
+    q = np.ascontiguousarray(queries[:sample])
+    n1 = max(1, sample // 10)
+    log(f"cpu baseline (port): oracle search of {n1} queries, 1 thread")
+    t = time.perf_counter()
+    orc.search(q[:n1], k, nprobe, krefine)
+    dt1 = time.perf_counter() - t
+    log(f"cpu baseline (port): oracle search of {sample} queries, {threads} threads")
+    t = time.perf_counter()
+    oids, od = orc.search_threads(q, k, nprobe, krefine, threads)
+    dtn = time.perf_counter() - t
+    g_ids, g_d = gpu_ids[:sample], gpu_d[:sample]
+    base_rec = {"value": sample / dtn, "unit": "queries/s", "cores": threads, "kind": "port",
+                "sample": f"first {sample} queries of the batch over {threads} threads "
+                          f"({dtn:.1f} s wall), same index (streamed out of the library, "
+                          f"dataset rows from memory), oracle/ivfpq_oracle.c",
+                "value_1_thread": n1 / dt1,
+                "sample_1_thread": f"first {n1} queries, 1 thread ({dt1:.1f} s)",
+                "host_nproc": os.cpu_count(), "host_cpu_model": cpu_model()}
+    fin = np.isfinite(od)
+    parity = {"queries": sample, "checker": "oracle", "tables": "f32",
+              "rows_identical": int(np.sum(np.all(oids == g_ids, axis=1))),
+              "distances_bit_identical": bool(np.array_equal(
+                  np.ascontiguousarray(g_d).view(np.uint32), np.ascontiguousarray(od).view(np.uint32))),
+              "rows_differing_beyond_ties": same_up_to_ties(g_ids, g_d, oids, od),
+              "max_rel_distance_error": float(np.max(np.abs(g_d[fin].astype(np.float64) - od[fin]) /
+                                                     np.maximum(1.0, np.abs(od[fin])))) if fin.any() else 0.0}
+    return base_rec, parity
+
+
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), or None."""
     try:
@@ -295,6 +363,10 @@ def main() -> int:
     ap.add_argument("--gen-workers", type=int, default=min(16, os.cpu_count() or 1),
                     help="processes generating the base rows of large configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-kind", choices=("auto", "reference", "port"), default="auto",
+                    help="CPU baseline and parity checker: the reference library (it loads an "
+                         "IPQ1 file), our C oracle on in-memory arrays, or auto (the reference "
+                         "below 8 GiB of vectors)")
     ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak kernels")
     ap.add_argument("--no-host-io", action="store_true",
@@ -382,6 +454,7 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
         log(f"calibration copies of {args.calibrate_copy_mb} MiB done")
         del src, dst
     s0 = res.ivfpq_search_stats()
+    h0 = res.ivfpq_table_queries()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -389,9 +462,11 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     s1 = res.ivfpq_search_stats()
+    table_queries = (res.ivfpq_table_queries() - h0) / args.steps
     elapsed = t1 - t0
     qps = nq * args.steps / elapsed
-    log(f"{args.steps} timed steps: {elapsed * 1e3 / args.steps:.3f} ms/step, {qps:,.0f} QPS")
+    log(f"{args.steps} timed steps: {elapsed * 1e3 / args.steps:.3f} ms/step, {qps:,.0f} QPS, "
+        f"{table_queries:.0f} queries per step handed to the full-table scan")
 
     # Smaller batches of the same queries (the config's other batch sizes; reported
     # beside `value`, which is the whole batch).
@@ -522,9 +597,16 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
 
     cpu, parity = (None, None)
     if not args.no_cpu_baseline:
-        cpu, parity = cpu_baseline(index, queries, gpu_ids, gpu_d, k, cfg.nprobe, krefine,
-                                   min(args.cpu_sample, nq), args.cpu_threads, cfg.lut_f16,
-                                   ovvs_amd)
+        kind = args.cpu_kind
+        if kind == "auto":
+            kind = "reference" if cfg.n * cfg.dim * 4 < (8 << 30) else "port"
+        if kind == "reference":
+            cpu, parity = cpu_baseline(index, queries, gpu_ids, gpu_d, k, cfg.nprobe, krefine,
+                                       min(args.cpu_sample, nq), args.cpu_threads, cfg.lut_f16,
+                                       ovvs_amd)
+        else:
+            cpu, parity = cpu_baseline_port(index, base, queries, gpu_ids, gpu_d, k, cfg.nprobe,
+                                            krefine, min(args.cpu_sample, nq), args.cpu_threads)
         if cpu:
             log(f"cpu baseline {cpu['value']:,.1f} QPS; parity {parity}")
 
@@ -556,6 +638,7 @@ def run(args, torch, ovvs_amd, cfg, nq, k, krefine, lut, base, queries) -> int:
         "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "stage_ms": stage_ms,
+        "table_queries_per_step": table_queries,
         "smaller_batches": small,
         "host_io": host,
         "recall_at_k": rec,

@@ -135,6 +135,12 @@ OVVS_API ovvsStatus ovvsResourcesLastComputeDtype(ovvsResources_t res, ovvsDType
 OVVS_API ovvsStatus ovvsResourcesIvfPqSearchStatsV1(ovvsResources_t res,
                                                     ovvsIvfPqSearchStatsV1* stats);
 
+/* ADDITIVE (no reference counterpart: the reference has one scan). The number of
+ * queries, over all IVF-PQ searches on res, whose lower bounds pruned too little
+ * and that the bounded scan therefore handed off to the full-table scan (data
+ * without cluster structure). Telemetry only: results do not depend on it. */
+OVVS_API ovvsStatus ovvsResourcesIvfPqTableQueries(ovvsResources_t res, int64_t* count);
+
 /* IVF-PQ (reference include/ovvs/ovvs.h:276-286). */
 OVVS_API ovvsStatus ovvsIvfPqBuild(ovvsResources_t res, const float* dataset, int64_t n,
                                    int64_t dim, ovvsMetric metric, int32_t nlist, int32_t pq_m,
@@ -245,6 +251,103 @@ OVVS_API ovvsStatus ovvsScannSearch(ovvsResources_t res, ovvsScannIndex_t index,
                                     const float* queries, int64_t nq, int64_t k, int32_t nprobe,
                                     int32_t krefine, int64_t* neighbors, float* distances);
 OVVS_API ovvsStatus ovvsScannDestroy(ovvsScannIndex_t index);
+
+/* Entry points of algorithms outside the IVF-PQ path (reference
+ * include/ovvs/ovvs.h:218-242,252-300,311-391,409-415,460-465). They are exported
+ * with the reference's names and signatures so that the reference's own callers
+ * (its Python package binds all of these when it loads the library) can load
+ * libovvs.so and use its IVF-PQ and ScaNN entry points. Each returns
+ * OVVS_STATUS_UNSUPPORTED and writes nothing (a Destroy given NULL returns
+ * OVVS_STATUS_SUCCESS; ovvsSyclEnabled returns 0). */
+typedef struct ovvsBruteForceIndexImpl* ovvsBruteForceIndex_t;
+typedef struct ovvsIvfFlatIndexImpl* ovvsIvfFlatIndex_t;
+typedef struct ovvsIvfRabitqIndexImpl* ovvsIvfRabitqIndex_t;
+typedef struct ovvsCagraIndexImpl* ovvsCagraIndex_t;
+typedef struct ovvsVamanaIndexImpl* ovvsVamanaIndex_t;
+typedef struct ovvsHnswIndexImpl* ovvsHnswIndex_t;
+typedef struct ovvsKMeansModelImpl* ovvsKMeansModel_t;
+typedef struct ovvsBatcherImpl* ovvsBatcher_t;
+OVVS_API int32_t ovvsSyclEnabled(void);
+OVVS_API ovvsStatus ovvsResourcesEnergyUj(ovvsResources_t res, int64_t* uj);
+OVVS_API ovvsStatus ovvsGemm(ovvsResources_t res, const float* a, const float* b, float* c,
+                             int64_t m, int64_t n, int64_t k, int32_t trans_b);
+OVVS_API ovvsStatus ovvsGemmEx(ovvsResources_t res, const float* a, const float* b, float* c,
+                               int64_t m, int64_t n, int64_t k, int32_t trans_b,
+                               ovvsDType compute);
+OVVS_API ovvsStatus ovvsTopk(ovvsResources_t res, const float* scores, int64_t rows,
+                             int64_t cols, int64_t k, int64_t* indices, float* values,
+                             int32_t largest);
+OVVS_API ovvsStatus ovvsGatherRows(ovvsResources_t res, const float* src, int64_t src_rows,
+                                   int64_t dim, const int64_t* idx, int64_t nidx, float* out);
+OVVS_API ovvsStatus ovvsBruteForceBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                        int64_t dim, ovvsMetric metric,
+                                        ovvsBruteForceIndex_t* index);
+OVVS_API ovvsStatus ovvsBruteForceSearch(ovvsResources_t res, ovvsBruteForceIndex_t index,
+                                         const float* queries, int64_t nq, int64_t k,
+                                         const uint8_t* bitset, int64_t* neighbors,
+                                         float* distances);
+OVVS_API ovvsStatus ovvsBruteForceDestroy(ovvsBruteForceIndex_t index);
+OVVS_API ovvsStatus ovvsIvfFlatBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                     int64_t dim, ovvsMetric metric, int32_t nlist,
+                                     ovvsIvfFlatIndex_t* index);
+OVVS_API ovvsStatus ovvsIvfFlatSearch(ovvsResources_t res, ovvsIvfFlatIndex_t index,
+                                      const float* queries, int64_t nq, int64_t k,
+                                      int32_t nprobe, const uint8_t* bitset,
+                                      int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsIvfFlatDestroy(ovvsIvfFlatIndex_t index);
+OVVS_API ovvsStatus ovvsIvfRabitqBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                       int64_t dim, ovvsMetric metric, int32_t nlist,
+                                       ovvsIvfRabitqIndex_t* index);
+OVVS_API ovvsStatus ovvsIvfRabitqSearch(ovvsResources_t res, ovvsIvfRabitqIndex_t index,
+                                        const float* queries, int64_t nq, int64_t k,
+                                        int32_t nprobe, int32_t krefine, const uint8_t* bitset,
+                                        int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsIvfRabitqSerialize(ovvsIvfRabitqIndex_t index, const char* path);
+OVVS_API ovvsStatus ovvsIvfRabitqDeserialize(ovvsResources_t res, const char* path,
+                                             ovvsIvfRabitqIndex_t* index);
+OVVS_API ovvsStatus ovvsIvfRabitqExtend(ovvsResources_t res, ovvsIvfRabitqIndex_t index,
+                                        const float* extra, int64_t nextra);
+OVVS_API ovvsStatus ovvsIvfRabitqDestroy(ovvsIvfRabitqIndex_t index);
+OVVS_API ovvsStatus ovvsCagraBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                   int64_t dim, ovvsMetric metric, int32_t graph_degree,
+                                   int32_t intermediate_degree, ovvsCagraIndex_t* index);
+OVVS_API ovvsStatus ovvsCagraSearch(ovvsResources_t res, ovvsCagraIndex_t index,
+                                    const float* queries, int64_t nq, int64_t k,
+                                    int32_t itopk_size, int32_t search_width,
+                                    const uint8_t* bitset, int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsCagraExtend(ovvsResources_t res, ovvsCagraIndex_t index,
+                                    const float* extra, int64_t nextra);
+OVVS_API ovvsStatus ovvsCagraDestroy(ovvsCagraIndex_t index);
+OVVS_API ovvsStatus ovvsHnswFromCagra(ovvsResources_t res, ovvsCagraIndex_t cagra,
+                                      ovvsHnswIndex_t* index);
+OVVS_API ovvsStatus ovvsHnswSearch(ovvsResources_t res, ovvsHnswIndex_t index,
+                                   const float* queries, int64_t nq, int64_t k, int32_t ef,
+                                   int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsHnswSerialize(ovvsHnswIndex_t index, const char* path);
+OVVS_API ovvsStatus ovvsHnswDeserialize(ovvsResources_t res, const char* path,
+                                        ovvsHnswIndex_t* index);
+OVVS_API ovvsStatus ovvsHnswDestroy(ovvsHnswIndex_t index);
+OVVS_API ovvsStatus ovvsVamanaBuild(ovvsResources_t res, const float* dataset, int64_t n,
+                                    int64_t dim, ovvsMetric metric, int32_t graph_degree,
+                                    float alpha, ovvsVamanaIndex_t* index);
+OVVS_API ovvsStatus ovvsVamanaSearch(ovvsResources_t res, ovvsVamanaIndex_t index,
+                                     const float* queries, int64_t nq, int64_t k, int32_t beam,
+                                     const uint8_t* bitset, int64_t* neighbors,
+                                     float* distances);
+OVVS_API ovvsStatus ovvsVamanaDestroy(ovvsVamanaIndex_t index);
+OVVS_API ovvsStatus ovvsKMeansFit(ovvsResources_t res, const float* dataset, int64_t n,
+                                  int64_t dim, int32_t nclusters, int32_t iters,
+                                  ovvsKMeansModel_t* model);
+OVVS_API ovvsStatus ovvsKMeansPredict(ovvsResources_t res, ovvsKMeansModel_t model,
+                                      const float* x, int64_t n, int64_t* labels,
+                                      float* distances);
+OVVS_API ovvsStatus ovvsKMeansDestroy(ovvsKMeansModel_t model);
+OVVS_API ovvsStatus ovvsBatcherCreate(ovvsResources_t res, ovvsBruteForceIndex_t index,
+                                      int32_t max_batch, int32_t max_wait_ms,
+                                      ovvsBatcher_t* out);
+OVVS_API ovvsStatus ovvsBatcherSearch(ovvsBatcher_t batcher, const float* queries, int64_t nq,
+                                      int64_t k, int64_t* neighbors, float* distances);
+OVVS_API ovvsStatus ovvsBatcherDestroy(ovvsBatcher_t batcher);
 
 /* Allow-list to an LSB-first bitset of (n+7)/8 bytes; ids outside [0,n) are
  * ignored (reference include/ovvs/ovvs.h:406, src/rt/resources.cpp:218-229). */

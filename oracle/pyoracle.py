@@ -104,6 +104,51 @@ def read_ipq1(path) -> Ipq1:
                 assign, lists)
 
 
+def read_ipq1_stream(f, dataset) -> Ipq1:
+    """read_ipq1 from a sequential stream (a pipe the library serializes into), with
+    the dataset section read and dropped in pieces: `dataset` ([n, dim] f32, the rows
+    the index was built from, by id) stands in for it. For indexes whose IPQ1 file
+    would not fit a disk (C5: 43 GB, 38.4 GB of it the dataset)."""
+
+    def read_exact(nbytes):
+        buf = bytearray(nbytes)
+        view = memoryview(buf)
+        got = 0
+        while got < nbytes:
+            m = f.readinto(view[got:])
+            if not m:
+                raise ValueError("IPQ1 stream ended early")
+            got += m
+        return buf
+
+    def take(dtype, count):
+        return np.frombuffer(read_exact(int(np.dtype(dtype).itemsize) * count), dtype=dtype)
+
+    head = bytes(read_exact(44))
+    magic, version = np.frombuffer(head[:8], dtype=np.int32)
+    if np.uint32(magic) != 0x31515049 or version != 1:
+        raise ValueError("not an IPQ1 v1 stream")
+    n, dim = (int(v) for v in np.frombuffer(head[8:24], dtype=np.int64))
+    nlist, pq_m, pq_ks, dsub, metric = (int(v) for v in np.frombuffer(head[24:44], dtype=np.int32))
+    if dataset.shape != (n, dim):
+        raise ValueError("dataset does not match the stream's shape")
+    centroids = take(np.float32, nlist * dim).reshape(nlist, dim)
+    codebooks = take(np.float32, pq_m * pq_ks * dsub).reshape(pq_m, pq_ks, dsub)
+    codes = take(np.uint8, n * pq_m).reshape(n, pq_m)
+    left = n * dim * 4
+    while left:
+        left -= len(read_exact(min(left, 1 << 26)))
+    assign = take(np.int32, n)
+    lists = []
+    for _ in range(nlist):
+        size = int(take(np.int32, 1)[0])
+        lists.append(take(np.int64, size))
+    if f.read(1):
+        raise ValueError("trailing bytes in IPQ1 stream")
+    return Ipq1(n, dim, nlist, pq_m, pq_ks, dsub, metric, centroids, codebooks, codes, dataset,
+                assign, lists)
+
+
 class _OracleIndex(ctypes.Structure):
     _fields_ = [
         ("n", c_int64), ("dim", c_int64), ("nlist", c_int32), ("pq_m", c_int32),
@@ -173,6 +218,39 @@ class Oracle:
         if self.lib.oracle_probe(ctypes.byref(self.s), _f32p(q), q.shape[0], P, _i64p(out)) != 0:
             raise MemoryError("oracle probe failed")
         return out
+
+    def search_threads(self, queries, k, nprobe, krefine, threads):
+        """search() over `threads` threads, each on a contiguous shard of the queries
+        (ctypes releases the GIL during each call; the C search keeps no shared state)."""
+        import threading
+
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.ix.dim)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), dtype=np.int64)
+        dists = np.empty((nq, k), dtype=np.float32)
+        bounds = np.linspace(0, nq, threads + 1).astype(np.int64)
+        rcs = [0] * threads
+
+        def work(t):
+            a, b = int(bounds[t]), int(bounds[t + 1])
+            if b > a:
+                sub = np.ascontiguousarray(q[a:b])
+                si = np.empty((b - a, k), dtype=np.int64)
+                sd = np.empty((b - a, k), dtype=np.float32)
+                rcs[t] = self.lib.oracle_ivfpq_search(ctypes.byref(self.s), _f32p(sub), b - a, k,
+                                                      nprobe, krefine, None, 0, _i64p(si),
+                                                      _f32p(sd))
+                ids[a:b] = si
+                dists[a:b] = sd
+
+        ts = [threading.Thread(target=work, args=(t,)) for t in range(threads)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+        if any(rcs):
+            raise MemoryError("oracle search failed")
+        return ids, dists
 
     def shortlist(self, query, probes, R, bitset=None, lut_f16=False):
         q = np.ascontiguousarray(query, dtype=np.float32).reshape(self.ix.dim)

@@ -111,6 +111,7 @@ _SIGS = {
     "ovvsResourcesLastDevice": (c_int32, [_V, POINTER(c_int32)]),
     "ovvsResourcesLastComputeDtype": (c_int32, [_V, POINTER(c_int32)]),
     "ovvsResourcesIvfPqSearchStatsV1": (c_int32, [_V, POINTER(_StatsV1)]),
+    "ovvsResourcesIvfPqTableQueries": (c_int32, [_V, POINTER(c_int64)]),
     "ovvsIvfPqBuild": (c_int32, [_V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
                                  c_int32, c_int32, POINTER(_V)]),
     "ovvsIvfPqSearch": (c_int32, [_V, _V, POINTER(c_float), c_int64, c_int64, c_int32, c_int32,
@@ -209,6 +210,14 @@ class Resources:
         v = c_int32()
         _check_status(_lib.ovvsResourcesLastComputeDtype(self._h, ctypes.byref(v)),
                       "last_compute_dtype")
+        return int(v.value)
+
+    def ivfpq_table_queries(self) -> int:
+        """Queries handed off to the full-table scan (bounds that did not prune), over
+        all searches on these Resources."""
+        v = c_int64()
+        _check_status(_lib.ovvsResourcesIvfPqTableQueries(self._h, ctypes.byref(v)),
+                      "ovvsResourcesIvfPqTableQueries")
         return int(v.value)
 
     def ivfpq_search_stats(self) -> dict:

@@ -16,7 +16,7 @@
 //                    P-th smallest score key, ordered compaction of the winners,
 //                    bitonic sort of (key, column) in LDS.
 //   k_probe_fallback the exact route for the queries the matrix-core probe flags:
-//                    one workgroup per 256 queries, each flagged one scored against
+//                    one workgroup per 16 queries, each flagged one scored against
 //                    every centroid and selected as in k_select_topk.
 //   k_coarse_argmin  the GEMM tile loop over all centroids for 64 rows with a
 //                    running (key, column) minimum: the k-means / extend assignment.
@@ -302,14 +302,17 @@ __device__ __forceinline__ void select_row(const float* __restrict__ S, int64_t 
 }
 
 // Rows that flags marks (flags[row] != 0) among the workgroup's 256 rows
-// [256 * blockIdx.x, +256), compacted into rows[0, *count). Called by the whole
-// workgroup; a workgroup without flagged rows returns count 0 after one load.
+// [kFallbackRows * blockIdx.x, +kFallbackRows), compacted into rows[0, *count). Called
+// by the whole workgroup; a workgroup without flagged rows returns count 0 after one
+// load.
+constexpr int kFallbackRows = 16;
 __device__ __forceinline__ int flagged_rows(const int32_t* __restrict__ flags, int64_t nrows,
                                             int32_t* rows, int32_t* count) {
   if (threadIdx.x == 0) *count = 0;
   __syncthreads();
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (row < nrows && flags[row] != 0) rows[atomicAdd(count, 1)] = static_cast<int32_t>(row);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kFallbackRows + threadIdx.x;
+  if (threadIdx.x < kFallbackRows && row < nrows && flags[row] != 0)
+    rows[atomicAdd(count, 1)] = static_cast<int32_t>(row);
   __syncthreads();
   return *count;
 }
@@ -326,8 +329,8 @@ __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ S
 }
 
 // The exact route for the queries the matrix-core probe flagged (usually none):
-// one workgroup per 256 queries; for each flagged one, the exact score of every
-// centroid into its row of S, then the row selection.
+// one workgroup per kFallbackRows queries; for each flagged one, the exact score of
+// every centroid into its row of S, then the row selection.
 __global__ __launch_bounds__(256) void k_probe_fallback(
     const float* __restrict__ Q, const float* __restrict__ qn, int64_t nq,
     const float* __restrict__ C, const float* __restrict__ cn, int nlist, int dim,
@@ -337,7 +340,7 @@ __global__ __launch_bounds__(256) void k_probe_fallback(
   __shared__ uint32_t hist[256];
   __shared__ uint32_t scan_scratch[4];
   __shared__ uint32_t digit_need[2];
-  __shared__ int32_t rows[256];
+  __shared__ int32_t rows[kFallbackRows];
   __shared__ int32_t count;
   const SelectLds L{sel, hist, scan_scratch, digit_need};
   const int n = flagged_rows(flags, nq, rows, &count);
@@ -416,7 +419,7 @@ extern "C" hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, i
     return hipErrorInvalidValue;
   int M = 1;
   while (M < P) M <<= 1;
-  hipLaunchKernelGGL(k_probe_fallback, dim3(static_cast<uint32_t>((nq + 255) / 256)), dim3(256),
+  hipLaunchKernelGGL(k_probe_fallback, dim3(static_cast<uint32_t>((nq + kFallbackRows - 1) / kFallbackRows)), dim3(256),
                      static_cast<size_t>(M) * sizeof(uint64_t), stream, Q, qn, nq, C, cn, nlist,
                      dim, flags, S, P, M, out);
   return hipGetLastError();

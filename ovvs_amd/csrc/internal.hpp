@@ -90,8 +90,12 @@ struct IndexDevice {
   float box_cmax = 0.f;    // max |centroid coordinate| (ScanLayoutHost::cmax)
   DeviceBuffer centroids;  // [nlist * dim] f32
   DeviceBuffer cnorm;      // [nlist] f32
-  DeviceBuffer cmfma;      // centroids as split-bf16 matrix-core operands (empty if dim > 128)
   float cnorm_max = 0.f;   // max of cnorm, +inf if any is NaN or inf
+  DeviceBuffer cmfma;      // centred centroids as bf16 matrix-core operands (empty when the
+                           // probe cannot take the dimension)
+  DeviceBuffer cmu;        // [dim] f32 centring vector of the probe operands
+  DeviceBuffer cnc;        // [nlist] f32 centred squared norms
+  float cnc_max = 0.f;     // max of cnc, +inf if any is NaN or inf
   DeviceBuffer codebooks;  // [pq_m * ks * dsub] f32
   DeviceBuffer codes;      // [positions / 64 * code_blocks * 512] u8
   DeviceBuffer ids;        // [positions] i64
@@ -156,6 +160,8 @@ struct ovvsResourcesImpl {
 
   std::mutex stats_mutex;
   ovvsIvfPqSearchStatsV1 stats{};
+  // Queries the bounded scan handed off to the full-table scan, over all searches.
+  std::atomic<int64_t> table_queries{0};
 
   // One call at a time per Resources (the documented model is one Resources
   // per thread; this keeps accidental sharing safe instead of racy).

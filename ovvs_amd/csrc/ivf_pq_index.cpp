@@ -346,10 +346,18 @@ ovvsStatus ovvsIvfPqIndexImpl::ensure_device(ovvsResourcesImpl& res, GpuWork& wo
                                   d->xnorm.as<float>(), s));
   work.kernel_launches += 2;
   std::vector<uint32_t> cmfma(ovvs_hip_probe_cmfma_words(static_cast<int32_t>(dim), nlist));
+  std::vector<float> cmu, cnc;
   if (!cmfma.empty()) {
-    ovvs_probe_pack_cmfma(centroids.data(), nlist, static_cast<int32_t>(dim), cmfma.data());
+    cmu.resize(static_cast<size_t>(dim));
+    cnc.resize(static_cast<size_t>(nlist));
+    ovvs_probe_prepare(centroids.data(), nlist, static_cast<int32_t>(dim), cmfma.data(), cmu.data(),
+                       cnc.data(), &d->cnc_max);
     OVVS_TRY(alloc(d->cmfma, cmfma.size() * 4, work));
     OVVS_TRY(h2d(d->cmfma.get(), cmfma.data(), cmfma.size() * 4, s, work));
+    OVVS_TRY(alloc(d->cmu, cmu.size() * 4, work));
+    OVVS_TRY(h2d(d->cmu.get(), cmu.data(), cmu.size() * 4, s, work));
+    OVVS_TRY(alloc(d->cnc, cnc.size() * 4, work));
+    OVVS_TRY(h2d(d->cnc.get(), cnc.data(), cnc.size() * 4, s, work));
   }
   std::vector<float> cnorm(static_cast<size_t>(nlist));
   OVVS_TRY(d2h(cnorm.data(), d->cnorm.get(), cnorm.size() * 4, s, work));

@@ -9,13 +9,15 @@
 // Device pipeline per call, all on the Resources stream:
 //   1. query norms and probe selection, either
 //      a. matrix-core probe with exact       ovvs_hip_probe_mfma (it also computes the
-//         re-score (dim <= 128, enough        query norms and clears the counters), then
+//         re-score (dim <= 1024, enough       query norms and clears the counters), then
 //         centroid groups)                    for the queries it flags
 //                                             ovvs_hip_probe_fallback
 //      b. query norms, exact coarse scores   ovvs_hip_row_norms, ovvs_hip_coarse_scores
 //         chunked over queries, row select   + ovvs_hip_select_topk
 //   2. the scan's query order                ovvs_hip_query_order
-//   3. fused LUT + code scan + shortlist    ovvs_hip_scan
+//   3. fused LUT + code scan + shortlist    ovvs_hip_scan, then ovvs_hip_scan_table for
+//                                           the queries it hands off (bounds that do
+//                                           not prune: a whole table per list)
 //   4. exact re-rank + final select, and    ovvs_hip_refine
 //      the sum of the scan's statistics
 // There is no host compute path: without a usable GPU the call fails with
@@ -162,8 +164,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     fixed += align256(static_cast<size_t>(nq) * R * 4);                 // shortlist positions
     fixed += align256(static_cast<size_t>(nq) * 4);                     // shortlist counts
     fixed += align256(static_cast<size_t>(nq) * 16);                    // scan statistics
+    fixed += align256(static_cast<size_t>(nq) * 4);                     // full-table handoffs
     fixed += device_io ? 0 : align256(nqk * 8) + align256(nqk * 4);     // staged outputs
-    fixed += align256(4 * 8);                                           // counters
+    fixed += align256(8 * 8);                                           // counters
     fixed += (!device_io && bitset) ? align256(bitset_bytes) : 0;
     // Query chunk of the coarse score matrix (the exact route and the probe's
     // fallback work through it chunk by chunk).
@@ -190,9 +193,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     if (io == Io::kHost) {
       SEARCH_TRY(res->reserve_pinned(pin_bits + (bitset ? bitset_bytes : 0)));
     } else if (io == Io::kDevice) {
-      SEARCH_TRY(res->reserve_pinned(32));
+      SEARCH_TRY(res->reserve_pinned(64));
     }
-    unsigned long long scratch_counters[4] = {0, 0, 0, 0};
+    unsigned long long scratch_counters[5] = {0, 0, 0, 0, 0};
     unsigned char* pin = io == Io::kScratch ? reinterpret_cast<unsigned char*>(scratch_counters)
                                             : static_cast<unsigned char*>(res->pinned);
 
@@ -208,11 +211,15 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     int32_t* d_spos = cv.take<int32_t>(static_cast<size_t>(nq) * R);
     int32_t* d_scnt = cv.take<int32_t>(static_cast<size_t>(nq));
     int32_t* d_sstats = cv.take<int32_t>(static_cast<size_t>(nq) * 4);
+    int32_t* d_punt = cv.take<int32_t>(static_cast<size_t>(nq));
     // Device outputs are written by the refine kernel in place; host outputs are
     // staged and copied only after the search has succeeded.
     int64_t* d_oid = device_io ? neighbors : cv.take<int64_t>(nqk);
     float* d_odist = device_io ? distances : cv.take<float>(nqk);
-    unsigned long long* d_counters = cv.take<unsigned long long>(4);
+    // counters: [0] candidate rows, [1] non-empty probed lists, [2] shortlist entries,
+    // [3] out-of-range probe ids or shortlist positions, [4] queries handed off to the
+    // full-table scan (as unsigned int); [5, 8) unused.
+    unsigned long long* d_counters = cv.take<unsigned long long>(8);
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
     if (!device_io && bitset) d_bitset = cv.take<uint8_t>(bitset_bytes);
     float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
@@ -241,7 +248,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     const bool mfma_probe =
         dv.cmfma.get() != nullptr && ovvs_hip_probe_mfma_supported(dim, ix.nlist, P) != 0;
     // The matrix-core probe computes the query norms and clears the counters itself.
-    if (!mfma_probe) SEARCH_HIP(hipMemsetAsync(d_counters, 0, 4 * 8, s));
+    if (!mfma_probe) SEARCH_HIP(hipMemsetAsync(d_counters, 0, 8 * 8, s));
 
     hipEvent_t* ev = res->events;
     SEARCH_HIP(hipEventRecord(ev[0], s));
@@ -262,9 +269,12 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       pa.nlist = ix.nlist;
       pa.P = P;
       pa.centroids = dv.centroids.as<float>();
-      pa.cmfma = dv.cmfma.as<uint32_t>();
       pa.cnorm = dv.cnorm.as<float>();
       pa.cnorm_max = dv.cnorm_max;
+      pa.cmfma = dv.cmfma.as<uint32_t>();
+      pa.cmu = dv.cmu.as<float>();
+      pa.cnc = dv.cnc.as<float>();
+      pa.cnc_max = dv.cnc_max;
       pa.probes = d_probes;
       pa.fallback = d_flags;
       SEARCH_HIP(ovvs_hip_probe_mfma(&pa, s));
@@ -330,7 +340,13 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.out_pos = d_spos;
     sa.out_count = d_scnt;
     sa.out_stats = d_sstats;
+    // Queries whose bounds do not prune go to the full-table scan when its table fits.
+    const bool table_ok =
+        ovvs_hip_scan_table_lds_bytes(ix.pq_m, ix.pq_ks, dim, R, P) != 0;
+    sa.punt = table_ok ? d_punt : nullptr;
+    sa.punt_count = reinterpret_cast<unsigned int*>(d_counters + 4);
     SEARCH_HIP(ovvs_hip_scan(&sa, s));
+    if (table_ok) SEARCH_HIP(ovvs_hip_scan_table(&sa, s));
     SEARCH_HIP(hipEventRecord(ev[3], s));
 
     OvvsRefineArgs ra{};
@@ -355,11 +371,11 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.counters = d_counters;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += mfma_probe ? 3 + chunks : 5 + 2 * chunks;
+    work.kernel_launches += (mfma_probe ? 3 + chunks : 5 + 2 * chunks) + (table_ok ? 1 : 0);
 
-    SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 4 * 8, hipMemcpyDeviceToHost, s));
+    SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
     ovvs::saturating_add(work.d2h_calls, 1);
-    ovvs::saturating_add(work.d2h_bytes, 32);
+    ovvs::saturating_add(work.d2h_bytes, 40);
     if (!device_io) {
       SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
       SEARCH_HIP(hipMemcpyAsync(pin + pin_dist, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));
@@ -368,7 +384,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     }
     ovvs::saturating_add(work.wait_calls, 1);
     SEARCH_HIP(hipStreamSynchronize(s));
-    unsigned long long counters[4];
+    unsigned long long counters[5];
     std::memcpy(counters, pin, sizeof(counters));
     // A probe id or shortlist position out of range is an internal error: the
     // kernels count it instead of dereferencing it, and nothing is published.
@@ -419,6 +435,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       const int64_t* src = &d.successful_calls;
       for (int i = 0; i < 24; ++i) ovvs::saturating_add(dst[i], src[i]);
     }
+    res->table_queries += static_cast<int64_t>(counters[4] & 0xffffffffull);
     res->last_device = OVVS_DEVICE_GPU;
     res->last_compute_dtype = OVVS_DTYPE_F32;
     return OVVS_STATUS_SUCCESS;

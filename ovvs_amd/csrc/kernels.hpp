@@ -57,23 +57,23 @@ hipError_t ovvs_hip_coarse_scores(const float* Q, const float* qn, int64_t nq, c
 hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int32_t N, int32_t P,
                                 int32_t* out, hipStream_t stream);
 
-// ---- coarse probe on the fp32 matrix cores (probe.hip) ----
+// ---- coarse probe on the matrix cores (probe.hip) ----
 
-// Limits of the fused probe: dim <= 32 * OVVS_PROBE_MAX_KSTEPS (query fragments held
-// in registers), P <= OVVS_PROBE_MAX_P, at least 2P of its (at most OVVS_PROBE_MAX_GROUPS)
-// centroid groups, at most 256 (P <= 64) or OVVS_PROBE_CAP exact re-scores per query
-// (a query with more takes the exact route).
-#define OVVS_PROBE_MAX_KSTEPS 4
+// Limits of the fused probe: dim <= 32 * OVVS_PROBE_MAX_KSTEPS, P <= OVVS_PROBE_MAX_P, at
+// least 2P of its (at most OVVS_PROBE_MAX_GROUPS) centroid groups, its LDS within 160 KiB,
+// at most 256 (P <= 64), 512 (P <= 128) or OVVS_PROBE_CAP (512 where that does not fit
+// the LDS) exact re-scores per query (a query with more takes the exact route).
+#define OVVS_PROBE_MAX_KSTEPS 32
 #define OVVS_PROBE_MAX_P 256
 #define OVVS_PROBE_MAX_GROUPS 512
-#define OVVS_PROBE_CAP 512
+#define OVVS_PROBE_CAP 1024
 
 struct OvvsProbeArgs {
   const float* queries;    // [nq * dim]
   const float* qnorm;      // [nq], exact row norms; or nullptr: the probe computes them
                            // (sequential sums, as ovvs_hip_row_norms) into qnorm_out
   float* qnorm_out;        // [nq] out when qnorm is nullptr
-  unsigned long long* zero; // [4] set to 0 by the launch (the search's counters), or nullptr
+  unsigned long long* zero; // [8] set to 0 by the launch (the search's counters), or nullptr
   const int32_t* list_rank;  // with order_keys: [nlist] spatial rank of every list
   int32_t key_shift;         // order_keys[q] = list_rank[nearest probe] >> key_shift
   int32_t* order_keys;       // [nq] out (0 for flagged queries), or nullptr
@@ -82,24 +82,29 @@ struct OvvsProbeArgs {
   int32_t nlist;
   int32_t P;               // probes per query
   const float* centroids;  // [nlist * dim] row-major (exact re-score)
-  const uint32_t* cmfma;   // centroids as split-bf16 matrix-core operands, see
-                           // ovvs_probe_pack_cmfma
   const float* cnorm;      // [nlist], exact row norms
   float cnorm_max;         // max of cnorm (+inf if any is NaN or inf)
+  const uint32_t* cmfma;   // centred centroids as bf16 matrix-core operands, see
+                           // ovvs_probe_prepare
+  const float* cmu;        // [dim] the centring vector mu
+  const float* cnc;        // [nlist] centred squared norms
+  float cnc_max;           // max of cnc (+inf if any is NaN or inf)
   int32_t* probes;         // [nq * P] out, rank order (rows with fallback[q] = 0)
   int32_t* fallback;       // [nq] out: 1 where the query needs the exact route
 };
 
 // 1 when the fused probe handles these shapes.
 int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t P);
-// 32-bit words in the split-bf16 centroid operand copy (0 if dim is unsupported).
+// 32-bit words in the bf16 centroid operand copy (0 if dim is unsupported).
 size_t ovvs_hip_probe_cmfma_words(int32_t dim, int32_t nlist);
-// Host-side packing of that copy: for tile t (16 centroids), k-step s (32 dims), half
-// h (0: x_hi = bf16(x), 1: x_lo = bf16(x - x_hi), round to nearest even) and lane l,
-// the 16 bytes at word ((((t * ceil(dim/32) + s) * 2 + h) * 64 + l) * 4 hold the 8
-// bf16 values of x = C[16t + l%16][32s + 8(l/16) + j], j = 0..7 (zero past nlist or
-// dim).
-void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim, uint32_t* out);
+// Host-side preparation of the probe's centroid operands: mu[t] = the mean of column t
+// (double sum, rounded to float); cnc[c] = left-to-right fp32 sum of fl(C[c][t] -
+// mu[t])^2 and *cnc_max their maximum (+inf if any is not finite); ops: for tile t (16
+// centroids), k-step s (32 dims) and lane l, the 16 bytes at word ((t * ceil(dim/32) + s)
+// * 64 + l) * 4 hold the 8 bf16 values (round to nearest even) of fl(C[16t + l%16][k] -
+// mu[k]), k = 32s + 8(l/16) + j, j = 0..7 (zero past nlist or dim).
+void ovvs_probe_prepare(const float* C, int32_t nlist, int32_t dim, uint32_t* ops, float* mu,
+                        float* cnc, float* cnc_max);
 // Probe selection for every query; flags the queries the exact route must finish.
 hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream);
 // The exact route for the queries with flags[q] != 0 (the ones the fused probe could
@@ -157,11 +162,27 @@ struct OvvsScanArgs {
   int32_t* out_stats;          // [nq * 4] per query: rows of the probed lists, non-empty
                                // probed lists, shortlist entries, 1 if a probe id is out
                                // of range
+  // Handoff to the full-table scan (ovvs_hip_scan_table): a query whose rows past
+  // the scan's first phase exceed a work budget (its lower bounds prune too little)
+  // stops scoring and is appended to punt[] (*punt_count, cleared before the search);
+  // that kernel then rewrites all its outputs. nullptr: no handoff.
+  int32_t* punt;               // [nq]
+  unsigned int* punt_count;
 };
 
 // Code scan + per-query shortlist of the K best (ADC score, dense ordinal) rows
 // over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
+// Full-table scan of the queries ovvs_hip_scan handed off (punt[0 .. *punt_count)):
+// for every probed list, a lookup table of every subspace built in LDS, every row of
+// the list scored; the same outputs (out_keys, out_pos, out_count, out_stats) as
+// ovvs_hip_scan, bit for bit. A fixed number of workgroups take the handed-off
+// queries in turn (a search without any returns at once).
+hipError_t ovvs_hip_scan_table(const OvvsScanArgs* args, hipStream_t stream);
+// Dynamic LDS bytes of the full-table scan (0 if it does not fit the 160 KiB of a
+// gfx950 workgroup, the table holding pq_m * ks fp32 entries, or if dim > 1024 or
+// P > 1024).
+size_t ovvs_hip_scan_table_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t K, int32_t P);
 // order = the queries 0 .. nq-1 sorted by the spatial rank (list_rank, a permutation
 // of the lists) of their nearest probed list (probes[q * P]); the scan hands each
 // XCD one contiguous part of it, so that its L2 serves lists near each other.

@@ -1,4 +1,4 @@
-// probe.hip — coarse probe on the fp32 matrix cores with fused candidate selection,
+// probe.hip — coarse probe on the matrix cores with fused candidate selection,
 // exact re-score and an exact fallback, for IVF-PQ search on gfx950.
 //
 // The probe set of query q is the first P centroids under the total order on
@@ -7,36 +7,42 @@
 // src/prim/mixer.cpp:174-199, src/prim/cpu/cpu_prims.cpp:24-106).
 //
 // k_probe_mfma, one workgroup of NW wave64s per 16 queries (8; 16 when the batch
-// gives fewer workgroups than CUs, so that each wave's tile chain is half as long):
-//   pass 1   v_mfma_f32_16x16x32_bf16 tiles of 16 queries x 16 centroids give
-//            approximate scores a(q,c) from split operands: every fp32 value x is
-//            x_hi + x_lo with x_hi = bf16(x), x_lo = bf16(x - x_hi) (round to nearest
-//            even; x - x_hi is exact), and q.c ~ q_hi.c_hi + q_hi.c_lo + q_lo.c_hi,
-//            three bf16 products per element accumulated in fp32. The tiles are cut
-//            into nch chunks of gt consecutive tiles;
-//            group (chunk, column j) holds the centroids 16t + j of the chunk's tiles,
-//            and each lane keeps the running minimum of a over its group in registers.
-//            v_q is the P-th smallest of the 16 * nch group minima (as order keys): at
-//            least P distinct centroids (one per group) have a <= t_q, the score v_q
-//            encodes.
-//   bound    E_q >= |a(q,c) - s(q,c)| for every centroid c. The reference's sequential
-//            dot is within gamma_n |q||c| of the real one (n = dim + 4, u = 2^-23).
-//            The split dot drops q_lo c_lo and the split remainders, at most
-//            3.05 * 2^-16 |q_i c_i| per element, and accumulates 3 * 32 * ksteps exact
-//            bf16 products plus the accumulator in fp32; each addition is allowed 8x
-//            the fp32 unit roundoff (2^-20) whatever order or rounding the matrix
-//            core uses, plus an absolute term for flushed subnormals. The shared
-//            |q|^2 + |c|^2 term is rounded once more in both.
-//   pass 2   every centroid with !(a > T_q), T_q = t_q + 2 E_q rounded up, is a
-//            candidate. A centroid outside has s > t_q + E_q >= s of at least P
-//            candidates, so P entries precede it in the exact order: the exact first
-//            P are all candidates.
+// gives fewer workgroups than CUs):
+//   operands  mu = the mean of the centroids (per dimension). The queries' and the
+//            centroids' centred coordinates fl(x - mu) are rounded to bf16 (round
+//            to nearest even); the centroid operands are stored in MFMA fragment
+//            order with their centred norms |c'|^2 (left-to-right fp32 sums).
+//            Centring makes the bf16 error relative to |q - mu| |c - mu| instead
+//            of |q| |c| (data far from the origin, such as [0, 255] coordinates,
+//            would otherwise carry a large absolute error).
+//   pass 1   v_mfma_f32_16x16x32_bf16 tiles of 16 queries x 16 centroids give the
+//            approximate score a'(q,c) = |c'|^2 - 2 (q^ . c^), one bf16 product per
+//            element accumulated in fp32; a' approximates s(q,c) minus a constant of
+//            the query (|q - mu|^2), which no comparison below needs. The tiles are
+//            cut into nch chunks of gt consecutive tiles; group (chunk, column j)
+//            holds the centroids 16t + j of the chunk's tiles and each lane keeps the
+//            running minimum of a' over its groups; t_q = the P-th smallest of the
+//            16 * nch group minima: at least P distinct centroids have a' <= t_q.
+//            The minimum over each chunk per query is kept as well.
+//   bound    E_q >= |a'(q,c) + |q - mu|^2 - s(q,c)| for every centroid c
+//            (candidate_bound): the reference's own rounding of s (sequential sums
+//            of n = dim terms, within gamma_n of the real |q - c|^2 terms), the
+//            rounding of the centred coordinates and of |c'|^2, the bf16 rounding of
+//            both operands (at most (2^-7 + 2^-16) |q'_i c'_i| per product), the
+//            matrix core's fp32 accumulation (2^-20 per addition, whatever order or
+//            rounding it uses) and flushed subnormals. T_q = t_q + 2 E_q, rounded up.
+//   pass 2   every centroid with !(a' > T_q) is a candidate (chunks whose minimum
+//            exceeds T_q for all 16 queries are passed over). A centroid outside
+//            has s > t_q + |q - mu|^2 + E_q >= s of at least P candidates, so P
+//            entries precede it in the exact order: the exact first P are all
+//            candidates.
 //   pass 3   each candidate is re-scored with the reference's sequential fp32 sums;
 //            its rank is the number of candidates with a smaller (s, c) key, and the
 //            P of rank < P are the probes in order, bit for bit.
 // A query with more candidates than the re-score capacity, or fewer than P (only NaN
 // or infinite inputs can cause that), is flagged in `fallback`; k_probe_fallback
 // (coarse.hip) then ranks it from exact scores of every centroid.
+#include <cmath>
 #include <cstring>
 
 #include "device_common.hpp"
@@ -49,31 +55,38 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-
 constexpr int kRows = 16;                     // queries per workgroup (MFMA M dimension)
 constexpr int kMaxChunks = OVVS_PROBE_MAX_GROUPS / 16;
 
-// Launch shape and LDS carve of one probe launch.
-struct ProbeShape {
-  int ntile;   // 16-centroid tiles (nlist padded to 16)
-  int gt;      // tiles per chunk
-  int nch;     // chunks; 16 * nch group slots
-  int cap;     // re-score capacity per query
-  int dq;      // LDS row stride of the staged queries (dim rounded up to 4)
-  int real_groups;  // groups holding at least one real centroid
-  size_t lds;  // dynamic LDS bytes
-};
-
 constexpr size_t align16(size_t b) { return (b + 15) & ~static_cast<size_t>(15); }
 
-// LDS: qs [16][dq] f32 | count [16] i32 | thr [16] f32 | qn [16] f32 | area: gmin
-// [16][16*nch] u32 during passes 1-2, then slot [16][cap] u64 (candidate id, later its
-// exact key).
+// Launch shape and LDS carve of one probe launch.
+struct ProbeShape {
+  int ntile;        // 16-centroid tiles (nlist padded to 16)
+  int ks;           // 32-dimension k-steps (dim padded to 32)
+  int gt;           // tiles per chunk
+  int nch;          // chunks; 16 * nch group slots
+  int cap;          // re-score capacity per query
+  int dq;           // LDS row stride of the staged queries (dim rounded up to 4)
+  int real_groups;  // groups holding at least one real centroid
+  size_t mu_off;    // [dq] f32: the centring vector
+  size_t a_off;     // [ks][64] uint4: the queries' bf16 operand fragments
+  size_t misc_off;  // count [16] | thr [16] | qn [16] | qcn [16] | flag [4]
+  size_t chmin_off; // [16][nch] u32: per query, the minimum key of each chunk
+  size_t area_off;  // gmin [16][16*nch] u32 during passes 1-2, then slot [16][cap] u64
+  size_t lds;       // dynamic LDS bytes
+};
+
 struct Carve {
   float* qs;
+  float* mu;
+  const uint4* aop;
   int32_t* count;
   float* thr;
   float* qn;
+  float* qcn;
+  int32_t* flag;
+  uint32_t* chmin;
   uint32_t* gmin;
   uint64_t* slot;
 };
@@ -81,13 +94,17 @@ struct Carve {
 __device__ __forceinline__ Carve carve(unsigned char* base, const ProbeShape& sh) {
   Carve c;
   c.qs = reinterpret_cast<float*>(base);
-  unsigned char* p = base + align16(static_cast<size_t>(kRows) * sh.dq * 4);
-  c.count = reinterpret_cast<int32_t*>(p);
-  c.thr = reinterpret_cast<float*>(p + kRows * 4);
-  c.qn = reinterpret_cast<float*>(p + 2 * kRows * 4);
-  p += align16(3 * kRows * 4);
-  c.gmin = reinterpret_cast<uint32_t*>(p);
-  c.slot = reinterpret_cast<uint64_t*>(p);
+  c.mu = reinterpret_cast<float*>(base + sh.mu_off);
+  c.aop = reinterpret_cast<const uint4*>(base + sh.a_off);
+  unsigned char* m = base + sh.misc_off;
+  c.count = reinterpret_cast<int32_t*>(m);
+  c.thr = reinterpret_cast<float*>(m + kRows * 4);
+  c.qn = reinterpret_cast<float*>(m + 2 * kRows * 4);
+  c.qcn = reinterpret_cast<float*>(m + 3 * kRows * 4);
+  c.flag = reinterpret_cast<int32_t*>(m + 4 * kRows * 4);
+  c.chmin = reinterpret_cast<uint32_t*>(base + sh.chmin_off);
+  c.gmin = reinterpret_cast<uint32_t*>(base + sh.area_off);
+  c.slot = reinterpret_cast<uint64_t*>(base + sh.area_off);
   return c;
 }
 
@@ -102,44 +119,10 @@ __host__ __device__ __forceinline__ uint16_t bf16_bits(uint32_t u) {
   return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-// The split of x: hi = bf16(x), lo = bf16(x - hi).
-__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-  hi = bf16_bits(__float_as_uint(x));
-  const float r = x - __uint_as_float(static_cast<uint32_t>(hi) << 16);
-  lo = bf16_bits(__float_as_uint(r));
-}
-
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 w) {
   bf16x8 v;
   __builtin_memcpy(&v, &w, sizeof(v));
   return v;
-}
-
-// Approximate dot products of tile t: lane holds rows 4*(lane/16)+r, column lane%16.
-// Operand lane layout of v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][8(l/16)+j]
-// and B[8(l/16)+j][l%16], j = 0..7, per 32-deep k-step. The centroid operands come
-// from the split copy (OvvsProbeArgs::cmfma): per tile and k-step, 64 lanes x 16 B
-// of high parts, then 64 lanes x 16 B of low parts.
-template <int KS>
-__device__ __forceinline__ f32x4 tile_dot(const bf16x8 (&ah)[KS], const bf16x8 (&al)[KS],
-                                          const uint32_t* __restrict__ cm, int t) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const uint4* src =
-      reinterpret_cast<const uint4*>(cm) + static_cast<int64_t>(t) * KS * 2 * 64 + lane_id();
-  uint4 bh[KS], bl[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    bh[s] = src[(2 * s) * 64];
-    bl[s] = src[(2 * s + 1) * 64];
-  }
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const bf16x8 h = as_bf16x8(bh[s]), l = as_bf16x8(bl[s]);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[s], h, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[s], l, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[s], h, acc, 0, 0, 0);
-  }
-  return acc;
 }
 
 // Score of a 32-bit order key (the inverse of score_key); the NaN key gives +inf.
@@ -155,39 +138,68 @@ __device__ __forceinline__ float next_up(float f) {
   return __uint_as_float((u & 0x80000000u) ? u - 1u : u + 1u);
 }
 
-// Candidate bound T = t + 2E for one query (see the file comment), rounded up.
-__device__ float candidate_bound(float t, float qn, float cn_max, int dim, int ksteps) {
-  if (!(t < __builtin_inff()) || !(qn < __builtin_inff()) || !(cn_max < __builtin_inff()))
+// Candidate bound T = t + 2E for one query, rounded up (see the file comment).
+// qn: the query's exact squared norm (sequential fp32 sum), qcn: the sequential
+// fp32 sum of its squared centred coordinates, cn_max / ccn_max: the largest of the
+// centroids' exact and centred squared norms. u = 2^-23 covers any rounding mode.
+__device__ float candidate_bound(float t, float qn, float qcn, float cn_max, float ccn_max, int dim,
+                                 int ksteps) {
+  if (!(t < __builtin_inff()) || !(qn < __builtin_inff()) || !(qcn < __builtin_inff()) ||
+      !(cn_max < __builtin_inff()) || !(ccn_max < __builtin_inff()))
     return __builtin_inff();
   const double u = 1.1920928955078125e-7;   // 2^-23
   const double um = 9.5367431640625e-7;     // 2^-20, per matrix-core addition
   const double n = static_cast<double>(dim) + 4.0;
-  const double gamma = n * u / (1.0 - n * u);
-  const double m = 3.0 * 32.0 * ksteps + 3.0 * ksteps + 16.0;
-  const double gm = m * um / (1.0 - m * um);
-  const double emf = 3.05 * 1.52587890625e-5 + 1.02 * gm;  // 2^-16 split remainder
+  const double g = n * u / (1.0 - n * u);
+  // The reference's score s against the real |q - c|^2: qd, cd bound |q|^2, |c|^2.
   const double qd = static_cast<double>(qn) * (1.0 + 4.0 * n * u);
   const double cd = static_cast<double>(cn_max) * (1.0 + 4.0 * n * u);
   const double S = sqrt(qd * cd) * (1.0 + 1e-6);
-  const double E = 2.0 * (2.0 * (emf + gamma) * S + 2.0 * u * (qd + cd + 2.0 * S)) +
-                   m * 1e-30 * (1.0 + sqrt(qd) + sqrt(cd));
+  const double e2 = (g + 3.0 * u) * (qd + cd) + 2.0 * (g + u) * S + u * (qd + cd + 2.0 * S);
+  // a' against the real |c'|^2 - 2 q'.c': qc, cc bound |q - mu|^2, |c - mu|^2.
+  const double qc = static_cast<double>(qcn) * (1.0 + 4.0 * n * u);
+  const double cc = static_cast<double>(ccn_max) * (1.0 + 4.0 * n * u);
+  const double Sc = sqrt(qc * cc) * (1.0 + 1e-6);
+  const double m = 33.0 * ksteps + 8.0;
+  const double gm = m * um / (1.0 - m * um);
+  const double ep = 0.0078125 + 1.52587890625e-5 + 3.0 * u;  // 2^-7 + 2^-16 per product
+  const double e1 = (g + 5.0 * u) * cc + 2.0 * (ep + 1.02 * gm + 1.02 * u) * Sc +
+                    m * 1e-30 * (1.0 + sqrt(qc) + sqrt(cc) + sqrt(qd) + sqrt(cd));
+  const double E = 1.01 * (e1 + e2);
   const double T = static_cast<double>(t) + 2.0 * E;
   float f = static_cast<float>(T);
   if (static_cast<double>(f) < T && f < __builtin_inff()) f = next_up(f);
   return f;
 }
 
+// Tiles per batch of operand loads: every batch requests the B fragments of kG
+// tiles (and their centred norms) before its matrix-core products.
+template <int KS>
+constexpr int batch_tiles() {
+  return 4;
+}
+
+// KS in 1..4: the queries' operand fragments are held in registers (dim <= 128);
+// KS = 0: any number of k-steps, fragments read from LDS per k-step, the next
+// k-step's B fragments requested before the current products.
+// Six waves per SIMD (at most 80 VGPRs) for the register-operand shapes: with three
+// workgroups of eight waves per CU (their LDS allows it up to dim 128 and 256
+// candidates), a 10k-query batch's 625 workgroups run in one round on 256 CUs instead
+// of 1.2. The LDS-operand shapes keep the compiler's allocation (their LDS allows one
+// workgroup per CU).
 template <int KS, int NW>
-__global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, const ProbeShape shape) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 ? 6 : 1))) void k_probe_mfma(
+    const OvvsProbeArgs p, const ProbeShape shape) {
   constexpr int kWaves = NW;
   constexpr int kThreads = 64 * NW;
   constexpr int kRowsPerWave = kRows / kWaves;  // rows each wave selects and ranks
+  constexpr int kG = batch_tiles<KS>();
   extern __shared__ __align__(16) unsigned char smem[];
   const Carve L = carve(smem, shape);
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kRows;
-  const int dim = p.dim, dq = shape.dq;
+  const int dim = p.dim, dq = shape.dq, ks = shape.ks, nch = shape.nch;
 
   // Stage the 16 query rows (zero past dim and past nq).
   for (int i = static_cast<int>(threadIdx.x); i < kRows * dq; i += kThreads) {
@@ -195,69 +207,139 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
     const int64_t q = q0 + r;
     L.qs[i] = (q < p.nq && t < dim) ? p.queries[q * dim + t] : 0.f;
   }
+  for (int t = static_cast<int>(threadIdx.x); t < dim; t += kThreads) L.mu[t] = p.cmu[t];
   if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
-  if (p.zero && blockIdx.x == 0 && threadIdx.x < 4) p.zero[threadIdx.x] = 0;
+  if (threadIdx.x == 0) L.flag[0] = 0;
+  if (p.zero && blockIdx.x == 0 && threadIdx.x < 8) p.zero[threadIdx.x] = 0;
   __syncthreads();
-  // Query norms: given, or the sequential sums of squares of the staged rows.
+  // Query norms (given, or the sequential sums of squares of the staged rows), the
+  // centred sums, and the bf16 operand fragments of fl(q - mu): lane l of k-step s
+  // holds A[l % 16][32 s + 8 (l / 16) + j], j = 0..7.
   if (threadIdx.x < kRows) {
     const int64_t q = q0 + threadIdx.x;
-    float s = 0.f;
+    const float* r = L.qs + threadIdx.x * dq;
+    float s = 0.f, sc = 0.f;
     if (p.qnorm) {
       s = q < p.nq ? p.qnorm[q] : 0.f;
     } else {
-      const float* r = L.qs + threadIdx.x * dq;
       for (int t = 0; t < dim; ++t) s = s + r[t] * r[t];
       if (q < p.nq) p.qnorm_out[q] = s;
     }
+    for (int t = 0; t < dim; ++t) {
+      const float d = r[t] - L.mu[t];
+      sc = sc + d * d;
+    }
     L.qn[threadIdx.x] = q < p.nq ? s : 0.f;
+    L.qcn[threadIdx.x] = q < p.nq ? sc : 0.f;
+  }
+  {
+    uint4* aop = reinterpret_cast<uint4*>(smem + shape.a_off);
+    for (int i = static_cast<int>(threadIdx.x); i < ks * 64; i += kThreads) {
+      const int s = i >> 6, l = i & 63, row = l & 15;
+      const bool live = q0 + row < p.nq;
+      uint16_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = 32 * s + 8 * (l >> 4) + j;
+        const float x = (live && k < dim) ? L.qs[row * dq + k] - L.mu[k] : 0.f;
+        h[j] = bf16_bits(__float_as_uint(x));
+      }
+      uint4 w;
+      __builtin_memcpy(&w, h, sizeof(w));
+      aop[i] = w;
+    }
   }
   __syncthreads();
 
-  bf16x8 ah[KS], al[KS];
+  bf16x8 ah[KS > 0 ? KS : 1];
+  if constexpr (KS > 0) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    uint16_t h[8], l[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int k = 32 * s + 8 * (lane >> 4) + j;
-      split_bf16(k < dim ? L.qs[(lane & 15) * dq + k] : 0.f, h[j], l[j]);
-    }
-    __builtin_memcpy(&ah[s], h, sizeof(h));
-    __builtin_memcpy(&al[s], l, sizeof(l));
-  }
-  float qn[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t row = q0 + 4 * (lane >> 4) + r;
-    qn[r] = L.qn[4 * (lane >> 4) + r];
-    (void)row;
+    for (int s = 0; s < KS; ++s) ah[s] = as_bf16x8(L.aop[s * 64 + lane]);
   }
   const int col = lane & 15;
+  const uint4* __restrict__ bops = reinterpret_cast<const uint4*>(p.cmfma) + lane;
+  // Dot products of the kG tiles t0 + g (tiles at or past tend repeat tile t0 and
+  // are ignored by the caller), and the centred norm of each lane's centroid.
+  auto batch = [&](int t0, int tend, f32x4 (&acc)[kG], float (&cn)[kG]) {
+    int tt[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      tt[g] = t0 + g < tend ? t0 + g : t0;
+      acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int c = 16 * tt[g] + col;
+      cn[g] = c < p.nlist ? p.cnc[c] : 0.f;
+    }
+    if constexpr (KS > 0) {
+      uint4 b[kG][KS];
+#pragma unroll
+      for (int g = 0; g < kG; ++g)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) b[g][s] = bops[(static_cast<int64_t>(tt[g]) * KS + s) * 64];
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+          acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[s], as_bf16x8(b[g][s]), acc[g], 0, 0, 0);
+    } else {
+      uint4 cur[kG], nxt[kG];
+#pragma unroll
+      for (int g = 0; g < kG; ++g) cur[g] = bops[static_cast<int64_t>(tt[g]) * ks * 64];
+      for (int s = 0; s < ks; ++s) {
+        if (s + 1 < ks) {
+#pragma unroll
+          for (int g = 0; g < kG; ++g) nxt[g] = bops[(static_cast<int64_t>(tt[g]) * ks + s + 1) * 64];
+        }
+        const bf16x8 a = as_bf16x8(L.aop[s * 64 + lane]);
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+          acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(cur[g]), acc[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) cur[g] = nxt[g];
+      }
+    }
+  };
 
-  // Pass 1: running minimum of a over each (chunk, column) group.
-  for (int ch = wave; ch < shape.nch; ch += kWaves) {
+  // Pass 1: running minimum of a' over each (chunk, column) group, and of each
+  // query row over the chunk. A NaN score (only non-finite inputs make one) turns
+  // chunk skipping off for the workgroup.
+  const int ng = 16 * nch;
+  bool bad = false;
+  for (int ch = wave; ch < nch; ch += kWaves) {
     const int t0 = ch * shape.gt;
     const int t1 = min(t0 + shape.gt, shape.ntile);
     float m[4] = {__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff()};
-    for (int t = t0; t < t1; ++t) {
-      const f32x4 acc = tile_dot<KS>(ah, al, p.cmfma, t);
-      const int c = 16 * t + col;
-      if (c < p.nlist) {
-        const float cn = p.cnorm[c];
+    for (int t = t0; t < t1; t += kG) {
+      f32x4 acc[kG];
+      float cn[kG];
+      batch(t, t1, acc, cn);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) m[r] = __builtin_fminf(m[r], (qn[r] + cn) - 2.f * acc[r]);
+      for (int g = 0; g < kG; ++g) {
+        if (t + g < t1 && 16 * (t + g) + col < p.nlist) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = cn[g] - 2.f * acc[g][r];
+            bad |= a != a;
+            m[r] = __builtin_fminf(m[r], a);
+          }
+        }
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      L.gmin[(4 * (lane >> 4) + r) * (16 * shape.nch) + ch * 16 + col] = score_key(m[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * (lane >> 4) + r;
+      L.gmin[row * ng + ch * 16 + col] = score_key(m[r]);
+      float v = m[r];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) v = __builtin_fminf(v, __shfl_xor(v, o, 64));
+      if (col == 0) L.chmin[row * nch + ch] = score_key(v);
+    }
   }
+  if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) atomicOr(&L.flag[0], 1);
   __syncthreads();
 
   // The P-th smallest group minimum of each row, bit by bit from the top: v is the
   // smallest key with at least P group minima <= v. Each lane holds its slots; the
   // wave's rows are searched together (independent compare/count chains).
-  const int ng = 16 * shape.nch;
   {
     uint32_t g[kRowsPerWave][kMaxChunks / 4];
     uint32_t v[kRowsPerWave];
@@ -289,30 +371,51 @@ __global__ __launch_bounds__(64 * NW) void k_probe_mfma(const OvvsProbeArgs p, c
       for (int rr = 0; rr < kRowsPerWave; ++rr) {
         const int row = kRowsPerWave * wave + rr;
         const int64_t q = q0 + row;
-        const float qnr = q < p.nq ? L.qn[row] : 0.f;
-        L.thr[row] = candidate_bound(key_to_score(v[rr]), qnr, p.cnorm_max, dim, KS);
+        const bool live = q < p.nq;
+        L.thr[row] = candidate_bound(key_to_score(v[rr]), live ? L.qn[row] : 0.f,
+                                     live ? L.qcn[row] : 0.f, p.cnorm_max, p.cnc_max, dim, ks);
       }
     }
   }
   __syncthreads();
 
-  // Pass 2: every centroid whose approximate score is not above the bound.
+  // Pass 2: every centroid whose approximate score is not above the bound; a chunk
+  // whose minimum exceeds the bound for all 16 rows holds none.
   float T[4];
+  uint32_t kT[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) T[r] = L.thr[4 * (lane >> 4) + r];
+  for (int r = 0; r < 4; ++r) {
+    T[r] = L.thr[4 * (lane >> 4) + r];
+    kT[r] = score_key(T[r]);
+  }
+  const bool may_skip = L.flag[0] == 0;
   const int cap = shape.cap;
-  for (int t = wave; t < shape.ntile; t += kWaves) {
-    const f32x4 acc = tile_dot<KS>(ah, al, p.cmfma, t);
-    const int c = 16 * t + col;
-    if (c < p.nlist) {
-      const float cn = p.cnorm[c];
+  for (int ch = wave; ch < nch; ch += kWaves) {
+    if (may_skip) {
+      bool hit = false;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float s = (qn[r] + cn) - 2.f * acc[r];
-        if (!(s > T[r])) {
-          const int row = 4 * (lane >> 4) + r;
-          const int at = atomicAdd(&L.count[row], 1);
-          if (at < cap) L.slot[row * cap + at] = static_cast<uint64_t>(c);
+      for (int r = 0; r < 4; ++r) hit |= L.chmin[(4 * (lane >> 4) + r) * nch + ch] <= kT[r];
+      if (__builtin_amdgcn_ballot_w64(hit) == 0) continue;
+    }
+    const int t0 = ch * shape.gt;
+    const int t1 = min(t0 + shape.gt, shape.ntile);
+    for (int t = t0; t < t1; t += kG) {
+      f32x4 acc[kG];
+      float cn[kG];
+      batch(t, t1, acc, cn);
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        const int c = 16 * (t + g) + col;
+        if (t + g < t1 && c < p.nlist) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = cn[g] - 2.f * acc[g][r];
+            if (!(a > T[r])) {
+              const int row = 4 * (lane >> 4) + r;
+              const int at = atomicAdd(&L.count[row], 1);
+              if (at < cap) L.slot[row * cap + at] = static_cast<uint64_t>(c);
+            }
+          }
         }
       }
     }
@@ -369,19 +472,29 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
       P > OVVS_PROBE_MAX_P)
     return false;
   sh->ntile = (nlist + 15) / 16;
+  sh->ks = (dim + 31) / 32;
   sh->gt = (sh->ntile + kMaxChunks - 1) / kMaxChunks;
   sh->nch = (sh->ntile + sh->gt - 1) / sh->gt;
   int real = 0;
   for (int ch = 0; ch < sh->nch; ++ch) real += min(16, nlist - 16 * ch * sh->gt);
   sh->real_groups = real;
   if (2 * P > real) return false;
-  sh->cap = P <= 64 ? 256 : OVVS_PROBE_CAP;
+  // Re-score capacity: about four times P (the candidates are the P-th group
+  // minimum's centroids plus the bound's window), 512 when 1024 would not fit.
+  sh->cap = P <= 64 ? 256 : P <= 128 ? 512 : OVVS_PROBE_CAP;
   sh->dq = (dim + 3) & ~3;
-  const size_t area = static_cast<size_t>(kRows) *
-                      (static_cast<size_t>(16 * sh->nch) * 4 > static_cast<size_t>(sh->cap) * 8
-                           ? static_cast<size_t>(16 * sh->nch) * 4
-                           : static_cast<size_t>(sh->cap) * 8);
-  sh->lds = align16(static_cast<size_t>(kRows) * sh->dq * 4) + align16(3 * kRows * 4) + area;
+  sh->mu_off = align16(static_cast<size_t>(kRows) * sh->dq * 4);
+  sh->a_off = sh->mu_off + align16(static_cast<size_t>(sh->dq) * 4);
+  sh->misc_off = sh->a_off + static_cast<size_t>(sh->ks) * 64 * 16;
+  sh->chmin_off = sh->misc_off + align16(4 * kRows * 4 + 16);
+  sh->area_off = sh->chmin_off + align16(static_cast<size_t>(kRows) * sh->nch * 4);
+  const size_t gmin = static_cast<size_t>(kRows) * 16 * sh->nch * 4;
+  for (;;) {
+    const size_t slot = static_cast<size_t>(kRows) * sh->cap * 8;
+    sh->lds = sh->area_off + (gmin > slot ? gmin : slot);
+    if (sh->lds <= 160 * 1024 || sh->cap <= 512) break;
+    sh->cap = 512;
+  }
   return sh->lds <= 160 * 1024;
 }
 
@@ -417,35 +530,46 @@ extern "C" int ovvs_hip_probe_mfma_supported(int32_t dim, int32_t nlist, int32_t
 extern "C" size_t ovvs_hip_probe_cmfma_words(int32_t dim, int32_t nlist) {
   if (dim <= 0 || dim > 32 * OVVS_PROBE_MAX_KSTEPS || nlist <= 0) return 0;
   const size_t ks = static_cast<size_t>((dim + 31) / 32);
-  return static_cast<size_t>((nlist + 15) / 16) * ks * 2 * 64 * 4;
+  return static_cast<size_t>((nlist + 15) / 16) * ks * 64 * 4;
 }
 
-extern "C" void ovvs_probe_pack_cmfma(const float* C, int32_t nlist, int32_t dim,
-                                      uint32_t* out) {
+extern "C" void ovvs_probe_prepare(const float* C, int32_t nlist, int32_t dim, uint32_t* ops,
+                                   float* mu, float* cnc, float* cnc_max) {
   const int ks = (dim + 31) / 32, ntile = (nlist + 15) / 16;
+  for (int t = 0; t < dim; ++t) {
+    double s = 0.0;
+    for (int c = 0; c < nlist; ++c) s += static_cast<double>(C[static_cast<size_t>(c) * dim + t]);
+    mu[t] = static_cast<float>(s / static_cast<double>(nlist));
+  }
+  float mx = 0.f;
+  for (int c = 0; c < nlist; ++c) {
+    float s = 0.f;
+    for (int t = 0; t < dim; ++t) {
+      const float d = C[static_cast<size_t>(c) * dim + t] - mu[t];
+      s = s + d * d;
+    }
+    cnc[c] = s;
+    if (!(s <= mx)) mx = std::isfinite(s) ? s : INFINITY;
+    if (std::isinf(mx)) {
+      for (int r = c + 1; r < nlist; ++r) cnc[r] = INFINITY;
+      break;
+    }
+  }
+  *cnc_max = mx;
   for (int t = 0; t < ntile; ++t)
     for (int s = 0; s < ks; ++s)
       for (int lane = 0; lane < 64; ++lane) {
-        uint16_t hi[8], lo[8];
+        uint16_t h[8];
         for (int j = 0; j < 8; ++j) {
           const int k = 32 * s + 8 * (lane / 16) + j, c = 16 * t + lane % 16;
-          const float x = (c < nlist && k < dim) ? C[static_cast<size_t>(c) * dim + k] : 0.f;
+          const float x = (c < nlist && k < dim) ? C[static_cast<size_t>(c) * dim + k] - mu[k] : 0.f;
           uint32_t u;
           std::memcpy(&u, &x, 4);
-          hi[j] = bf16_bits(u);
-          const uint32_t hu = static_cast<uint32_t>(hi[j]) << 16;
-          float h;
-          std::memcpy(&h, &hu, 4);
-          const float r = x - h;
-          std::memcpy(&u, &r, 4);
-          lo[j] = bf16_bits(u);
+          h[j] = bf16_bits(u);
         }
-        uint32_t* dh = out + ((static_cast<size_t>(t) * ks + s) * 2 * 64 + lane) * 4;
-        uint32_t* dl = dh + 64 * 4;
-        for (int w = 0; w < 4; ++w) {
-          dh[w] = static_cast<uint32_t>(hi[2 * w]) | (static_cast<uint32_t>(hi[2 * w + 1]) << 16);
-          dl[w] = static_cast<uint32_t>(lo[2 * w]) | (static_cast<uint32_t>(lo[2 * w + 1]) << 16);
-        }
+        uint32_t* d = ops + ((static_cast<size_t>(t) * ks + s) * 64 + lane) * 4;
+        for (int w = 0; w < 4; ++w)
+          d[w] = static_cast<uint32_t>(h[2 * w]) | (static_cast<uint32_t>(h[2 * w + 1]) << 16);
       }
 }
 
@@ -454,13 +578,14 @@ extern "C" hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t
   const OvvsProbeArgs& p = *args;
   if (p.nq <= 0) return hipSuccess;
   ProbeShape sh;
-  if (!p.queries || (!p.qnorm && !p.qnorm_out) || !p.centroids || !p.cmfma || !p.cnorm || !p.probes ||
-      !p.fallback || p.nq > 0x7fffffff || !probe_shape(p.dim, p.nlist, p.P, &sh))
+  if (!p.queries || (!p.qnorm && !p.qnorm_out) || !p.centroids || !p.cmfma || !p.cnorm || !p.cmu ||
+      !p.cnc || !p.probes || !p.fallback || p.nq > 0x7fffffff || !probe_shape(p.dim, p.nlist, p.P, &sh))
     return hipErrorInvalidValue;
-  switch ((p.dim + 31) / 32) {
+  switch (sh.ks) {
     case 1: return launch_probe<1>(p, sh, stream);
     case 2: return launch_probe<2>(p, sh, stream);
     case 3: return launch_probe<3>(p, sh, stream);
-    default: return launch_probe<4>(p, sh, stream);
+    case 4: return launch_probe<4>(p, sh, stream);
+    default: return launch_probe<0>(p, sh, stream);
   }
 }

@@ -387,6 +387,12 @@ OVVS_API ovvsStatus ovvsResourcesIvfPqSearchStatsV1(ovvsResources_t res,
   return OVVS_STATUS_SUCCESS;
 }
 
+OVVS_API ovvsStatus ovvsResourcesIvfPqTableQueries(ovvsResources_t res, int64_t* count) {
+  if (!res || !count) return OVVS_STATUS_INVALID_ARGUMENT;
+  *count = res->table_queries.load();
+  return OVVS_STATUS_SUCCESS;
+}
+
 OVVS_API ovvsStatus ovvsBitsetFromAllowList(int64_t n, const int64_t* ids, int64_t nids,
                                             uint8_t* bitset) {
   if (!bitset || n <= 0 || nids < 0) return OVVS_STATUS_INVALID_ARGUMENT;

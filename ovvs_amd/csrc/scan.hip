@@ -407,6 +407,9 @@ constexpr int kItemCap = 256;
 // Phase 0: candidate groups per rank (of the first kWaves ranks) and rounds.
 constexpr int kP0Cand = 64;
 constexpr int kP0Rounds = 4;
+// Tiles a query may score after phase 0 before it is handed off to the full-table scan
+// (at least; more when its live lists are large).
+constexpr int kPuntTiles = 32;
 static_assert(kWaves * kP0Cand * 8 <= kWaves * 2 * kSegSlots * 4, "phase-0 candidates must fit the slot area");
 // Rounding allowances of the lower bounds (valid for up to OVVS_MAX_BOX_DIMS box
 // dimensions and as many subspaces): a threshold raised by 2^-10 relative and a
@@ -424,8 +427,9 @@ struct ScanLayout {
   size_t query_off;  // the query row [dim_pad]
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
-  size_t misc_off;   // [8] int32: end of phase 0, bad probe flag, rows, lists, groups
-                     //     scored in phase 0 (kP0Rounds)
+  size_t misc_off;   // [16] int32: end of phase 0, bad probe flag, rows, lists, groups
+                     //      scored in phase 0 (kP0Rounds), tiles scored after phase 0,
+                     //      rows of the lists whose bound passed after phase 0
   size_t slot_off;   // per wave: [2][kSegSlots] int32, the segments of a bound pass and
                      //           their list ranks; before: phase 0's candidate groups
                      //           [kWaves * kP0Cand] u64
@@ -451,7 +455,7 @@ __host__ __device__ inline ScanLayout scan_layout(int dim, int kpl, int P) {
   L.resid_off = L.query_off + dim_pad * 4;
   L.thr_off = L.resid_off + static_cast<size_t>(kWaves) * dim_pad * 4;
   L.misc_off = L.thr_off + (kWaves + 1) * 8;
-  L.slot_off = L.misc_off + 32;
+  L.slot_off = L.misc_off + 64;
   L.item_off = L.slot_off + static_cast<size_t>(kWaves) * 2 * kSegSlots * 4;
   L.table_off = L.item_off + static_cast<size_t>(kItemCap) * 6;
   L.total = L.table_off + (8 * static_cast<size_t>(P) + 1 + (P + 63) / 64) * 4;
@@ -838,6 +842,8 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
   }
   if (threadIdx.x < kP0Rounds) misc[4 + threadIdx.x] = -1;
+  if (threadIdx.x == kP0Rounds) misc[8] = 0;      // tiles scored after phase 0
+  if (threadIdx.x == kP0Rounds + 1) misc[9] = 0;  // rows of the lists whose bound passed
   __syncthreads();
   // Rounds: the candidate with the smallest bound (ties: the first) is scored; a
   // further round runs while the best remaining candidate's bound does not exceed
@@ -993,6 +999,10 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     const int t = 64 * c + lane;
     int32_t n = 0;
     if (t < a.P && t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi)) n = t_ngrp[t];
+    int32_t live = n > 0 ? t_rows[t] : 0;  // rows of the lists whose bound passed
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) live += __shfl_xor(live, o, 64);
+    if (lane == 0) atomicAdd(&misc[9], live);
     const int32_t incl = wave_incl_scan(n);
     if (t < a.P) {
       t_item[t] = incl - n;  // within the chunk
@@ -1006,6 +1016,15 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   const int32_t cincl = wave_incl_scan(ctot);
   const int32_t cexcl = cincl - ctot;
   const int32_t n_items = __builtin_amdgcn_readlane(cincl, 63);
+  // Handoff to the full-table scan, for data whose lower bounds do not prune (no
+  // cluster structure, or no boxes): once the segments scored after phase 0 hold
+  // more than `budget` tiles (kPuntTiles, or an eighth of the tiles of the lists
+  // whose bound passed if that is more), the waves stop scoring, and the query is
+  // handed off at the end (its outputs are then written by the full-table scan).
+  const int32_t budget = a.punt ? max(kPuntTiles, misc[9] / (8 * kTile)) : 0x7fffffff;
+  auto over_budget = [&]() {
+    return __hip_atomic_load(&misc[8], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > budget;
+  };
   int cur_p = -1;  // list whose residual is in resid
   for (int ib = 0; ib < n_items; ib += kItemCap) {
     const int nb = n_items - ib < kItemCap ? n_items - ib : kItemCap;
@@ -1023,6 +1042,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
     __syncthreads();
     for (int s0 = wave * kSegPerPass; s0 < nb; s0 += kWaves * kSegPerPass) {
+    if (over_budget()) break;
     const int filled = nb - s0 < kSegPerPass ? nb - s0 : kSegPerPass;
     refresh();
     // Group bounds; the segments of the groups kept (in item order, so lists stay
@@ -1085,7 +1105,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         const int b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lead && rank == r));
         // The threshold may have dropped since the pass (this wave's or another's).
         refresh();
-        if (readlane_f(etot, b) > thr_hi) continue;
+        if (readlane_f(etot, b) > thr_hi || over_budget()) continue;
         const float tl_j = readlane_f(tl, b);
         const int gs = __builtin_amdgcn_readlane(seg, b);
         const int p = __builtin_amdgcn_readlane(pp, b);
@@ -1104,6 +1124,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
         const int32_t st = a.seg_start[gs];
         const int32_t len = a.seg_len[gs];
+        if (lane == 0) atomicAdd(&misc[8], (len + kTile - 1) / kTile);
         for (int32_t t0 = 0; t0 < len; t0 += kTile) {
           const int32_t pos0 = st + t0;
           const int32_t pos = pos0 + lane;
@@ -1198,6 +1219,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
+    if (lane == 0 && misc[8] > budget) a.punt[atomicAdd(a.punt_count, 1u)] = static_cast<int32_t>(q);
     if (lane == 0) {
       a.out_count[q] = valid;
       // Per-query statistics, summed by the statistics workgroups of the refine
@@ -1253,6 +1275,548 @@ hipError_t launch_scan(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// ---- full-table scan (queries the bounded scan hands off) ----
+//
+// One workgroup per query (the grid's workgroups take the handed-off queries in
+// turn). For every non-empty probed list in rank order: the whole table T[m][j] of
+// the list in LDS (all 256 threads, entry by entry in the reference's operation
+// order), then every row of the list scored from it, the rows offered to the wave's
+// running top-K under the same (score, raw ordinal) keys as the bounded scan. No
+// bound is evaluated: this serves data whose bounds rule nothing out, where building
+// each list's table once costs less than computing entries row by row.
+//
+// Latency is what limits this loop (two barriers per list, few waves per CU), so
+// every global load is issued ahead of its use: the codebook entries of the table
+// stay in registers for the kernel's whole run when they fit (pq_m * ks * dsub <=
+// 256 * kCbRegs; dim <= 96 at 256 centres per subspace), the next list's centroid is
+// loaded while the current list is scored, and each wave loads the codes and
+// ordinals of its next 64-row slot while it scores the current one. A list's rows
+// are dealt in slots: slot 2s + h is rows [64h, 64h + 64) of the list's segment s
+// (segments hold at most 128 rows), slot j to wave j % 4.
+struct TableLayout {
+  size_t lut_off;    // [pq_m][ks] f32; at the end, the cross-wave merge (aliased)
+  size_t bufk_off;   // per wave: candidate keys [kBufCap]
+  size_t bufp_off;   // per wave: candidate positions [kBufCap]
+  size_t query_off;  // [dim_pad] f32
+  size_t resid_off;  // [dim_pad] f32, the current list's residual
+  size_t thr_off;    // [kWaves] u64 published K-th keys
+  size_t meta_off;   // [4][P] int32: first segment, end segment, ordinal base, rows
+  size_t total;
+};
+
+// Probes a handed-off query may have, and dimensions the full-table scan supports.
+constexpr int kTableMaxProbes = 1024;
+constexpr int kTableMaxDim = 1024;
+// Floats of codebook entries each thread keeps in registers.
+constexpr int kCbRegs = 96;
+// Code blocks (8 subspaces each) whose words are loaded one slot ahead.
+constexpr int kPfBlocks = 6;
+// Table entries a thread computes together when the codebook is read from memory
+// (their loads in flight at once).
+constexpr int kTableBatch = 8;
+
+__host__ __device__ inline TableLayout table_layout(int pq_m, int ks, int dim, int kpl, int P) {
+  TableLayout L;
+  const size_t dim_pad = static_cast<size_t>((dim + 3) & ~3);
+  const size_t lut = static_cast<size_t>(pq_m) * ks * 4;
+  const size_t merge = static_cast<size_t>(kWaves) * 64 * kpl * (8 + 4);
+  L.lut_off = 0;
+  L.bufk_off = round16(lut > merge ? lut : merge);
+  L.bufp_off = L.bufk_off + static_cast<size_t>(kWaves) * kBufCap * 8;
+  L.query_off = L.bufp_off + static_cast<size_t>(kWaves) * kBufCap * 4;
+  L.resid_off = L.query_off + dim_pad * 4;
+  L.thr_off = L.resid_off + dim_pad * 4;
+  L.meta_off = L.thr_off + kWaves * 8;
+  L.total = L.meta_off + static_cast<size_t>(P) * 16;
+  return L;
+}
+
+// Subspaces whose codebook entries a thread can hold in kCbRegs registers (a multiple
+// of 8, so that subspaces go in whole code blocks).
+__host__ __device__ constexpr int cb_reg_subspaces(int ds) { return ds > 0 ? (kCbRegs / ds) & ~7 : 0; }
+
+// True when thread-held codebook registers cover the whole table: 256 centres per
+// subspace (thread t holds centre t of every subspace), dsub 1, 2, 4 or 8, and whole
+// code blocks of subspaces (pq_m a multiple of 8) within the register budget.
+__host__ __device__ inline bool table_cb_in_regs(int pq_m, int ks, int dsub) {
+  return ks == kThreads && (dsub == 1 || dsub == 2 || dsub == 4 || dsub == 8) && pq_m % kBlock == 0 &&
+         pq_m <= cb_reg_subspaces(dsub);
+}
+
+// Register copy of the codebook for table_cb_in_regs shapes: c[m] holds the DS
+// coordinates of centre threadIdx.x of subspace m, loaded once per workgroup.
+template <int DS>
+struct CbRegs {
+  float c[DS > 0 ? cb_reg_subspaces(DS) : 1][DS > 0 ? DS : 1];
+};
+
+template <int DS>
+__device__ __forceinline__ void load_cb_regs(CbRegs<DS>& r, const float* __restrict__ codebooks, int pq_m) {
+  if constexpr (DS > 0) {
+#pragma unroll
+    for (int m = 0; m < cb_reg_subspaces(DS); ++m) {
+      const float* __restrict__ cw =
+          codebooks + (static_cast<int64_t>(m < pq_m ? m : 0) * kThreads + threadIdx.x) * DS;
+#pragma unroll
+      for (int u = 0; u < DS; ++u) r.c[m][u] = m < pq_m ? cw[u] : 0.f;
+    }
+  }
+}
+
+// The table of one list: entry e = (m, j) is the sum over the subspace's coordinates
+// u of (r[m * dsub + u] - codebook[e][u])^2, in order from +0 (the reference's table,
+// src/neighbors/indexes.cpp:764-785). From the register copy when DS > 0 (thread t
+// computes centre t of every subspace, eight subspaces per step under one uniform
+// test), else from memory kTableBatch entries at a time.
+template <int DS>
+__device__ __forceinline__ void build_table(float* lut, const float* resid, const CbRegs<DS>& cr,
+                                            const float* __restrict__ codebooks, int n_e,
+                                            int ks_log2, int dsub, int pq_m) {
+  if constexpr (DS > 0) {
+#pragma unroll
+    for (int g = 0; g < cb_reg_subspaces(DS); g += kBlock) {
+      if (g < pq_m) {
+        float acc[kBlock];
+#pragma unroll
+        for (int j = 0; j < kBlock; ++j) {
+          const float* r = resid + (g + j) * DS;
+          float t = 0.f;
+#pragma unroll
+          for (int u = 0; u < DS; ++u) {
+            const float d = r[u] - cr.c[g + j][u];
+            t = t + d * d;
+          }
+          acc[j] = t;
+        }
+#pragma unroll
+        for (int j = 0; j < kBlock; ++j) lut[(g + j) * kThreads + threadIdx.x] = acc[j];
+      }
+    }
+  } else {
+    for (int e0 = static_cast<int>(threadIdx.x); e0 < n_e; e0 += kThreads * kTableBatch) {
+      float c[kTableBatch][8];
+      if (dsub <= 8) {
+#pragma unroll
+        for (int i = 0; i < kTableBatch; ++i) {
+          const int e = e0 + i * kThreads;
+          const float* __restrict__ cw = codebooks + static_cast<int64_t>(e < n_e ? e : 0) * dsub;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) c[i][u] = u < dsub ? cw[u] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kTableBatch; ++i) {
+        const int e = e0 + i * kThreads;
+        if (e < n_e) {
+          const float* r = resid + (e >> ks_log2) * dsub;
+          float acc = 0.f;
+          if (dsub <= 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              if (u < dsub) {
+                const float d = r[u] - c[i][u];
+                acc = acc + d * d;
+              }
+            }
+          } else {
+            const float* __restrict__ cw = codebooks + static_cast<int64_t>(e) * dsub;
+            for (int u = 0; u < dsub; ++u) {
+              const float d = r[u] - cw[u];
+              acc = acc + d * d;
+            }
+          }
+          lut[e] = acc;
+        }
+      }
+    }
+  }
+}
+
+// One 64-row slot of a list, as loaded ahead of its scoring.
+struct TableSlot {
+  uint2 w[kPfBlocks];  // code words of the first kPfBlocks blocks
+  int32_t pos;         // this lane's row position
+  int32_t ord;         // its ordinal within the list (rord)
+  bool ok;             // the lane holds a row that passes the filter
+};
+
+template <int KPL, int DS>
+__device__ __forceinline__ void table_query(const OvvsScanArgs& a, int64_t q, unsigned char* smem,
+                                            const CbRegs<DS>& cr) {
+  const TableLayout L = table_layout(a.pq_m, a.ks, a.dim, KPL, a.P);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = lane_id();
+  float* lut = reinterpret_cast<float*>(smem + L.lut_off);
+  uint64_t* bufk = reinterpret_cast<uint64_t*>(smem + L.bufk_off) + wave * kBufCap;
+  int32_t* bufp = reinterpret_cast<int32_t*>(smem + L.bufp_off) + wave * kBufCap;
+  float* qs = reinterpret_cast<float*>(smem + L.query_off);
+  float* resid = reinterpret_cast<float*>(smem + L.resid_off);
+  uint64_t* wave_thr = reinterpret_cast<uint64_t*>(smem + L.thr_off);
+  int32_t* m_seg0 = reinterpret_cast<int32_t*>(smem + L.meta_off);
+  int32_t* m_seg1 = m_seg0 + a.P;
+  int32_t* m_ord = m_seg1 + a.P;
+  int32_t* m_rows = m_ord + a.P;
+  const int K = a.K, P = a.P, pq_m = a.pq_m, dim = a.dim;
+  const int ks_log2 = __ffs(a.ks) - 1;
+  const int n_e = pq_m << ks_log2;
+  const int nblocks = (pq_m + kBlock - 1) / kBlock;
+  const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
+  const int tid = static_cast<int>(threadIdx.x);
+
+  // Per-rank metadata: segment range (empty for an empty or out-of-range list), rows,
+  // and the ordinal base (rows of the lists before it), by contiguous chunks of ranks
+  // per thread and a prefix sum of the chunk totals.
+  const int chunk = (P + kThreads - 1) / kThreads;
+  int32_t my_rows = 0, my_lists = 0, my_bad = 0;
+  for (int p = tid * chunk; p < P && p < (tid + 1) * chunk; ++p) {
+    const int l = a.probes[q * P + p];
+    int32_t s0 = 0, s1 = 0, rows = 0;
+    if (static_cast<uint32_t>(l) >= static_cast<uint32_t>(a.nlist)) {
+      my_bad = 1;
+    } else {
+      rows = static_cast<int32_t>(a.list_offsets[l + 1] - a.list_offsets[l]);
+      if (rows > 0) {
+        s0 = a.list_seg[l];
+        s1 = a.list_seg[l + 1];
+        ++my_lists;
+      }
+    }
+    m_seg0[p] = s0;
+    m_seg1[p] = s1;
+    m_rows[p] = rows;
+    my_rows += rows;
+  }
+  for (int t = tid; t < dim; t += kThreads) qs[t] = a.queries[q * dim + t];
+  if (lane == 0) wave_thr[wave] = kNoKey;
+  // Block prefix of the chunk totals: the waves' sums (and list counts and bad-probe
+  // flags) meet in their candidate areas, unused until the metadata is complete.
+  const int32_t incl = wave_incl_scan(my_rows);
+  int32_t* wsum = reinterpret_cast<int32_t*>(bufp);  // this wave's candidate area is unused yet
+  const int32_t wave_total = __builtin_amdgcn_readlane(incl, 63);
+  if (lane == 0) wsum[0] = wave_total;
+  int32_t rows_total = 0, lists = 0, bad = 0;
+  {
+    int32_t l = my_lists, b = my_bad;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      l += __shfl_xor(l, o, 64);
+      b |= __shfl_xor(b, o, 64);
+    }
+    lists = l;
+    bad = b;
+  }
+  if (lane == 0) {
+    wsum[1] = lists;
+    wsum[2] = bad;
+  }
+  __syncthreads();
+  int32_t before = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    const int32_t* ws = reinterpret_cast<const int32_t*>(smem + L.bufp_off) + w * kBufCap;
+    if (w < wave) before += ws[0];
+    rows_total += ws[0];
+    if (w != wave) {
+      lists += ws[1];
+      bad |= ws[2];
+    }
+  }
+  {
+    int32_t o = before + incl - my_rows;
+    for (int p = tid * chunk; p < P && p < (tid + 1) * chunk; ++p) {
+      m_ord[p] = o;
+      o += m_rows[p];
+    }
+  }
+  __syncthreads();  // metadata complete; the candidate areas are free again
+
+  uint64_t lk[KPL];
+  int32_t lp[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    lk[j] = kNoKey;
+    lp[j] = -1;
+  }
+  uint64_t thr = kNoKey;  // the smallest K-th key any wave has published
+  int cnt = 0;
+  uint32_t ord_base = 0;
+  auto publish = [&]() {
+    const uint64_t own = kth_key<KPL>(lk, K);
+    if (lane == 0) wave_thr[wave] = own;
+    uint64_t t = own;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t = wave_thr[w] < t ? wave_thr[w] : t;
+    thr = t;
+  };
+  auto flush = [&]() {
+    const int take = cnt < 64 ? cnt : 64;
+    uint64_t bk = lane < take ? bufk[lane] : kNoKey;
+    int32_t bp = lane < take ? bufp[lane] : -1;
+    const int rest = cnt - take;
+    if (lane < rest) {
+      const uint64_t mk = bufk[64 + lane];
+      const int32_t mp = bufp[64 + lane];
+      bufk[lane] = mk;
+      bufp[lane] = mp;
+    }
+    cnt = rest;
+    sort64(bk, bp);
+    merge64<KPL>(lk, lp, bk, bp);
+    publish();
+  };
+  auto offer = [&](bool ok, float score, int32_t pos, int32_t ord) {
+    uint64_t key = kNoKey;
+    if (ok) key = make_key(score, ord_base + static_cast<uint32_t>(ord));
+    const bool pass = key < thr;
+    const uint64_t bal = __ballot(pass);
+    if (bal) {
+      const int before_l = __popcll(bal & ((1ull << lane) - 1ull));
+      if (pass) {
+        bufk[cnt + before_l] = key;
+        bufp[cnt + before_l] = pos;
+      }
+      cnt += __popcll(bal);
+      if (cnt >= 64) flush();
+    }
+  };
+  auto settle = [&]() {
+    if (cnt > 0 && cnt <= 8) {
+      for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
+      cnt = 0;
+      publish();
+    } else {
+      while (cnt > 0) flush();
+    }
+  };
+  // First rank at or after p whose list has rows (P when none).
+  auto next_list = [&](int p) {
+    while (p < P && m_seg1[p] == m_seg0[p]) ++p;
+    return p;
+  };
+  // Slot k of list p for this wave: slot j = wave + 4k, rows [64 (j & 1), + 64) of the
+  // list's segment j >> 1. Every load is issued whatever the slot holds (lanes without a
+  // row read the segment's first row, blocks past the last re-read it), so that the
+  // compiler can count the loads in flight exactly and wait only for the ones it uses.
+  auto load_slot = [&](TableSlot& s, int pl, int k) {
+    const int nslot = 2 * (m_seg1[pl] - m_seg0[pl]);
+    const int j = wave + kWaves * k;
+    const bool has = j < nslot;
+    const int sg = __builtin_amdgcn_readfirstlane(m_seg0[pl] + (has ? (j >> 1) : 0));
+    const int h = has ? (j & 1) : 0;
+    const int32_t st = a.seg_start[sg];
+    const int32_t len = a.seg_len[sg];
+    s.pos = st + kTile * h + lane;
+    s.ok = has && lane < len - kTile * h;
+    const int32_t at = s.ok ? s.pos : st;
+    const unsigned char* __restrict__ cb =
+        a.codes + static_cast<size_t>(at >> 6) * tile_bytes + (at & (kTile - 1)) * kBlock;
+#pragma unroll
+    for (int b = 0; b < kPfBlocks; ++b)
+      s.w[b] = *reinterpret_cast<const uint2*>(cb + (b < nblocks ? b : nblocks - 1) * (kTile * kBlock));
+    s.ord = a.rord[at];
+  };
+  auto score_slot = [&](TableSlot& s) {
+    if (a.bitset && s.ok) {
+      const int64_t id = a.ids[s.pos];
+      s.ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
+    }
+    float sc = 0.f;
+    const unsigned char* __restrict__ cb =
+        a.codes + static_cast<size_t>(s.pos >> 6) * tile_bytes + (s.pos & (kTile - 1)) * kBlock;
+    if constexpr (DS > 0) {
+      // 256 centres per subspace and whole blocks: a block's eight entries are read
+      // (at fixed offsets from the block's table rows), then added in subspace order.
+      for (int b0 = 0; b0 < nblocks; b0 += kPfBlocks) {
+#pragma unroll
+        for (int i = 0; i < kPfBlocks; ++i) {
+          if (b0 + i < nblocks) {
+            const uint2 w = b0 == 0 ? s.w[i]
+                                    : (s.ok ? *reinterpret_cast<const uint2*>(cb + (b0 + i) * (kTile * kBlock))
+                                            : make_uint2(0u, 0u));
+            const uint32_t wv[2] = {w.x, w.y};
+            const float* lrow = lut + (b0 + i) * kBlock * kThreads;
+            float v[kBlock];
+#pragma unroll
+            for (int jj = 0; jj < kBlock; ++jj)
+              v[jj] = lrow[jj * kThreads + static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu)];
+#pragma unroll
+            for (int jj = 0; jj < kBlock; ++jj) sc = sc + v[jj];
+          }
+        }
+      }
+      offer(s.ok, sc, s.pos, s.ord);
+      return;
+    }
+    for (int b0 = 0; b0 < nblocks; b0 += kPfBlocks) {
+      uint2 w[kPfBlocks];
+#pragma unroll
+      for (int i = 0; i < kPfBlocks; ++i)
+        w[i] = b0 == 0 ? s.w[i]
+                       : (s.ok && b0 + i < nblocks
+                              ? *reinterpret_cast<const uint2*>(cb + (b0 + i) * (kTile * kBlock))
+                              : make_uint2(0u, 0u));
+#pragma unroll
+      for (int i = 0; i < kPfBlocks; ++i) {
+        const int m0 = (b0 + i) * kBlock;
+        if (m0 >= pq_m) break;
+        const int mb = pq_m - m0 < kBlock ? pq_m - m0 : kBlock;
+        const uint32_t wv[2] = {w[i].x, w[i].y};
+        if (mb == kBlock) {
+#pragma unroll
+          for (int jj = 0; jj < kBlock; ++jj) {
+            const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+            sc = sc + lut[((m0 + jj) << ks_log2) + code];
+          }
+        } else {
+          for (int jj = 0; jj < mb; ++jj) {
+            const int code = static_cast<int>((wv[jj >> 2] >> (8 * (jj & 3))) & 0xffu);
+            sc = sc + lut[((m0 + jj) << ks_log2) + code];
+          }
+        }
+      }
+    }
+    offer(s.ok, sc, s.pos, s.ord);
+  };
+
+  // Prologue: the first list's residual, the next list's centroid, this wave's first
+  // two slots of the first list.
+  int p = next_list(0);
+  if (p >= P) p = P;
+  constexpr int kCv = kTableMaxDim / kThreads;
+  float cvn[kCv];
+  // Centroid coordinates of the list of rank pl (the last list when pl == P, whose
+  // values are then unused), loaded by every lane.
+  auto load_centroid = [&](int pl) {
+    const int l = a.probes[q * P + (pl < P ? pl : P - 1)];
+    const int lc = static_cast<uint32_t>(l) < static_cast<uint32_t>(a.nlist) ? l : 0;
+    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(lc) * dim;
+#pragma unroll
+    for (int i = 0; i < kCv; ++i) {
+      const int t = tid + i * kThreads;
+      cvn[i] = cv[t < dim ? t : dim - 1];
+    }
+  };
+  if (p < P) {
+    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(a.probes[q * P + p]) * dim;
+    for (int t = tid; t < dim; t += kThreads) resid[t] = qs[t] - cv[t];
+  }
+  int pn = p < P ? next_list(p + 1) : P;
+  load_centroid(pn);
+  TableSlot nx0, nx1;
+  if (p < P) {
+    load_slot(nx0, p, 0);
+    load_slot(nx1, p, 1);
+  }
+
+  while (p < P) {
+    __syncthreads();  // list p's residual is complete; every wave is done with the previous table
+    // This list's first two slots (loaded a list ago), then the next list's.
+    TableSlot c0 = nx0, c1 = nx1;
+    if (pn < P) {
+      load_slot(nx0, pn, 0);
+      load_slot(nx1, pn, 1);
+    }
+    build_table<DS>(lut, resid, cr, a.codebooks, n_e, ks_log2, a.dsub, pq_m);
+    __syncthreads();
+    // The residual area is free: the next list's residual, then the centroid after it.
+    const int pnn = pn < P ? next_list(pn + 1) : P;
+    if (pn < P) {
+#pragma unroll
+      for (int i = 0; i < kCv; ++i)
+        if (tid + i * kThreads < dim) resid[tid + i * kThreads] = qs[tid + i * kThreads] - cvn[i];
+      load_centroid(pnn);
+    }
+    ord_base = static_cast<uint32_t>(m_ord[p]);
+    const int nslot = 2 * (m_seg1[p] - m_seg0[p]);
+    if (wave < nslot) score_slot(c0);
+    if (wave + kWaves < nslot) score_slot(c1);
+    for (int k = 2; wave + kWaves * k < nslot; ++k) {
+      TableSlot t;
+      load_slot(t, p, k);
+      score_slot(t);
+    }
+    settle();
+    p = pn;
+    pn = pnn;
+  }
+
+  // Cross-wave merge (the table area is free), as in the bounded scan.
+  constexpr int M = 64 * KPL;
+  __syncthreads();
+  uint64_t* mk = reinterpret_cast<uint64_t*>(smem + L.lut_off);
+  int32_t* mp = reinterpret_cast<int32_t*>(smem + L.lut_off + static_cast<size_t>(kWaves) * M * 8);
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    mk[wave * M + j * 64 + lane] = lk[j];
+    mp[wave * M + j * 64 + lane] = lp[j];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    for (int w = 1; w < kWaves; ++w) {
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int src = w * M + (KPL - 1 - j) * 64 + (63 - lane);
+        const uint64_t rk = mk[src];
+        if (rk < lk[j]) {
+          lk[j] = rk;
+          lp[j] = mp[src];
+        }
+      }
+      bitonic_merge_asc<KPL>(lk, lp);
+    }
+    int valid = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int e = j * 64 + lane;
+      if (e < K) {
+        a.out_keys[q * K + e] = lk[j];
+        a.out_pos[q * K + e] = lp[j];
+        valid += lk[j] != kNoKey;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
+    if (lane == 0) {
+      a.out_count[q] = valid;
+      a.out_stats[q * 4 + 0] = rows_total;
+      a.out_stats[q * 4 + 1] = lists;
+      a.out_stats[q * 4 + 2] = valid;
+      a.out_stats[q * 4 + 3] = bad;
+    }
+  }
+}
+
+// Two waves per SIMD: the table's LDS holds two workgroups per CU at C2's shape, and
+// the register copy of the codebook takes 96 of the 256 registers that leaves a wave.
+template <int KPL, int DS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_scan_table(
+    const OvvsScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const unsigned int n = *a.punt_count;
+  if (blockIdx.x >= n) return;
+  CbRegs<DS> cr;
+  load_cb_regs<DS>(cr, a.codebooks, a.pq_m);
+  for (unsigned int i = blockIdx.x; i < n; i += gridDim.x) {
+    table_query<KPL, DS>(a, a.punt[i], smem, cr);
+    __syncthreads();  // LDS is reused by the next query
+  }
+}
+
+// Workgroups of the full-table launch (each takes handed-off queries in turn).
+constexpr unsigned kTableGrid = 1024;
+
+template <int KPL, int DS>
+hipError_t launch_scan_table(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_scan_table<KPL, DS>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  const unsigned grid = a.nq < static_cast<int64_t>(kTableGrid) ? static_cast<unsigned>(a.nq) : kTableGrid;
+  hipLaunchKernelGGL((k_scan_table<KPL, DS>), dim3(grid), dim3(kThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
 int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512 ? 8 : 16; }
 
 }  // namespace
@@ -1291,6 +1855,50 @@ extern "C" hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream
     case 4: return launch_scan<4>(a, lds, stream);
     case 8: return launch_scan<8>(a, lds, stream);
     default: return launch_scan<16>(a, lds, stream);
+  }
+}
+
+extern "C" size_t ovvs_hip_scan_table_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t K,
+                                                int32_t P) {
+  if (pq_m <= 0 || ks <= 0 || dim <= 0 || dim > kTableMaxDim || K <= 0 || K > OVVS_HIP_MAX_REFINE ||
+      P <= 0 || P > kTableMaxProbes)
+    return 0;
+  const size_t b = table_layout(pq_m, ks, dim, kpl_for(K), P).total;
+  return b <= 160u * 1024u ? b : 0;
+}
+
+extern "C" hipError_t ovvs_hip_scan_table(const OvvsScanArgs* args, hipStream_t stream) {
+  if (!args) return hipErrorInvalidValue;
+  const OvvsScanArgs& a = *args;
+  if (a.nq <= 0 || !a.punt) return hipSuccess;
+  if (!a.punt_count || !a.queries || !a.probes || !a.centroids || !a.codebooks || !a.list_offsets ||
+      !a.codes || !a.ids || !a.rord || !a.list_seg || !a.seg_start || !a.seg_len || !a.out_keys ||
+      !a.out_pos || !a.out_count || !a.out_stats || a.nq > 0x7fffffff || a.nlist <= 0 || a.dim <= 0 ||
+      a.P <= 0 || a.pq_m <= 0 || a.dsub <= 0 || a.ks < 16 || a.ks > 256 || (a.ks & (a.ks - 1)) != 0 ||
+      a.code_blocks != (a.pq_m + kBlock - 1) / kBlock || static_cast<int64_t>(a.pq_m) * a.dsub > a.dim ||
+      a.K <= 0 || a.K > OVVS_HIP_MAX_REFINE)
+    return hipErrorInvalidValue;
+  const size_t lds = ovvs_hip_scan_table_lds_bytes(a.pq_m, a.ks, a.dim, a.K, a.P);
+  if (lds == 0) return hipErrorInvalidValue;
+  const int kpl = kpl_for(a.K);
+  if (kpl <= 2 && table_cb_in_regs(a.pq_m, a.ks, a.dsub)) {
+    switch (a.dsub * 4 + kpl) {
+      case 1 * 4 + 1: return launch_scan_table<1, 1>(a, lds, stream);
+      case 2 * 4 + 1: return launch_scan_table<1, 2>(a, lds, stream);
+      case 4 * 4 + 1: return launch_scan_table<1, 4>(a, lds, stream);
+      case 8 * 4 + 1: return launch_scan_table<1, 8>(a, lds, stream);
+      case 1 * 4 + 2: return launch_scan_table<2, 1>(a, lds, stream);
+      case 2 * 4 + 2: return launch_scan_table<2, 2>(a, lds, stream);
+      case 4 * 4 + 2: return launch_scan_table<2, 4>(a, lds, stream);
+      default: return launch_scan_table<2, 8>(a, lds, stream);
+    }
+  }
+  switch (kpl) {
+    case 1: return launch_scan_table<1, 0>(a, lds, stream);
+    case 2: return launch_scan_table<2, 0>(a, lds, stream);
+    case 4: return launch_scan_table<4, 0>(a, lds, stream);
+    case 8: return launch_scan_table<8, 0>(a, lds, stream);
+    default: return launch_scan_table<16, 0>(a, lds, stream);
   }
 }
 

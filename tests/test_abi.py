@@ -328,3 +328,47 @@ def test_knn_graph_argument_checks(ovvs):
     if not res.gpu_available():
         assert lib.ovvsIvfPqKnnGraph(res._h, xp, 8, 4, 0, 4, gp) == 7
         assert np.all(g == 7)
+
+
+# Every symbol the reference's Python package binds unconditionally when it loads the
+# library (reference python/ovvs/__init__.py:150-306, the `_lib.<name>.argtypes` and
+# `.restype` assignments at module level): with all of them exported, that package
+# loads libovvs.so through OVVS_LIBRARY and its IVF-PQ and ScaNN calls reach this
+# library (the others answer OVVS_STATUS_UNSUPPORTED).
+REFERENCE_PACKAGE_BINDS = (
+    "ovvsBatcherCreate", "ovvsBatcherDestroy", "ovvsBatcherSearch", "ovvsBitsetFromAllowList",
+    "ovvsBruteForceBuild", "ovvsBruteForceDestroy", "ovvsBruteForceSearch", "ovvsCagraBuild",
+    "ovvsCagraDestroy", "ovvsCagraExtend", "ovvsCagraSearch", "ovvsGatherRows", "ovvsGemm",
+    "ovvsGemmEx", "ovvsGetVersion", "ovvsHnswDeserialize", "ovvsHnswDestroy",
+    "ovvsHnswFromCagra", "ovvsHnswSearch", "ovvsHnswSerialize", "ovvsIvfFlatBuild",
+    "ovvsIvfFlatDestroy", "ovvsIvfFlatSearch", "ovvsIvfPqBuild", "ovvsIvfPqDeserialize",
+    "ovvsIvfPqDestroy", "ovvsIvfPqExtend", "ovvsIvfPqSearch", "ovvsIvfPqSerialize",
+    "ovvsIvfRabitqBuild", "ovvsIvfRabitqDeserialize", "ovvsIvfRabitqDestroy",
+    "ovvsIvfRabitqExtend", "ovvsIvfRabitqSearch", "ovvsIvfRabitqSerialize",
+    "ovvsKMeansDestroy", "ovvsKMeansFit", "ovvsKMeansPredict", "ovvsResourcesCreate",
+    "ovvsResourcesDestroy", "ovvsResourcesEnergyUj", "ovvsResourcesLastComputeDtype",
+    "ovvsResourcesLastDevice", "ovvsResourcesSetPolicy", "ovvsScannBuild", "ovvsScannDestroy",
+    "ovvsScannSearch", "ovvsStatusString", "ovvsSyclEnabled", "ovvsTopk", "ovvsVamanaBuild",
+    "ovvsVamanaDestroy", "ovvsVamanaSearch",
+)
+
+
+def test_reference_python_package_symbols_are_exported(ovvs):
+    lib = ctypes.CDLL(str(ovvs.library_path()))
+    assert len(REFERENCE_PACKAGE_BINDS) == 53
+    missing = [s for s in REFERENCE_PACKAGE_BINDS if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_other_algorithms_answer_unsupported(ovvs):
+    lib = ovvs._lib
+    res = ovvs.Resources()
+    h = c_void_p()
+    x = np.zeros((4, 8), dtype=np.float32)
+    assert lib.ovvsCagraBuild(res._h, x.ctypes.data_as(POINTER(c_float)), c_int64(4), c_int64(8),
+                              c_int32(0), c_int32(4), c_int32(8), byref(h)) == ovvs.STATUS_UNSUPPORTED
+    assert h.value is None
+    assert lib.ovvsBruteForceDestroy(None) == ovvs.STATUS_SUCCESS
+    assert lib.ovvsSyclEnabled() == 0
+    e = c_int64(-5)
+    assert lib.ovvsResourcesEnergyUj(res._h, byref(e)) == ovvs.STATUS_UNSUPPORTED and e.value == -5

@@ -508,3 +508,73 @@ def test_extend_is_transactional(ovvs, res, tmp_path):
         ref.close()
     re.close()
     ix.close()
+
+
+def test_table_mode_unclustered_and_mixed_against_oracle(ovvs, res, tmp_path):
+    """Queries whose lower bounds prune little (isotropic data, no clusters) are
+    handed off by the bounded scan to the full-table scan (each probed list's whole
+    table in LDS, every row scored); an index over clusters plus an isotropic
+    background serves, in one batch, queries the bounds prune (from the clusters)
+    and queries they do not (from the background). Both must match the oracle bit
+    for bit, with filters and long shortlists too, and the isotropic searches must
+    actually have taken the full-table scan."""
+    rng = np.random.default_rng(41)
+    dim = 32
+    iso = rng.standard_normal((40000, dim)).astype(np.float32)
+    q_iso = rng.standard_normal((300, dim)).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(iso, nlist=64, pq_m=16, pq_nbits=8, resources=res)
+    p = tmp_path / "iso.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    bitset = np.packbits((rng.random(40000) < 0.5).astype(np.uint8), bitorder="little")
+    for k, nprobe, krefine, bits in [(10, 16, 10, None), (10, 32, 64, bitset), (100, 8, 300, None),
+                                     (1, 64, 1, None)]:
+        say("iso", dict(k=k, nprobe=nprobe, krefine=krefine, bitset=bits is not None))
+        before = res.ivfpq_table_queries()
+        ids, d = ix.search(q_iso, k, nprobe, krefine, bitset=bits)
+        handed = res.ivfpq_table_queries() - before
+        say("handed off", handed)
+        if nprobe >= 16:
+            assert handed > 0, "isotropic queries never reached the full-table scan"
+        oids, od = orc.search(q_iso, k, nprobe, krefine, bits)
+        assert_results_match(ids, d, oids, od, label=f"iso k{k} p{nprobe}")
+        assert np.array_equal(_bits(d), _bits(od)), f"iso k{k} p{nprobe}"
+    ix.close()
+
+    # The other register layouts of the codebook (one, four and eight coordinates per
+    # entry) and the table read from memory (dsub 16).
+    for pq_m in (32, 8, 4, 2):
+        say("iso pq_m", pq_m)
+        ix = ovvs.neighbors.ivf_pq.build(iso[:20000], nlist=32, pq_m=pq_m, pq_nbits=8, resources=res)
+        p = tmp_path / f"iso{pq_m}.ipq1"
+        ix.serialize(p)
+        orc = Oracle(read_ipq1(p))
+        before = res.ivfpq_table_queries()
+        ids, d = ix.search(q_iso[:100], 10, 16, 32)
+        say("handed off", res.ivfpq_table_queries() - before)
+        oids, od = orc.search(q_iso[:100], 10, 16, 32)
+        assert_results_match(ids, d, oids, od, label=f"iso pq_m{pq_m}")
+        assert np.array_equal(_bits(d), _bits(od)), f"iso pq_m{pq_m}"
+        ix.close()
+
+    centers = 4.0 * rng.standard_normal((32, dim)).astype(np.float32)
+    clustered = (centers[rng.integers(0, 32, 30000)] +
+                 0.2 * rng.standard_normal((30000, dim))).astype(np.float32)
+    data = np.concatenate([clustered, 2.0 * iso[:30000]])
+    q = np.concatenate([(centers[rng.integers(0, 32, 200)] +
+                         0.2 * rng.standard_normal((200, dim))).astype(np.float32),
+                        2.0 * q_iso[:200]])
+    q = q[rng.permutation(len(q))]
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=128, pq_m=16, pq_nbits=8, resources=res)
+    p = tmp_path / "mixed.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for k, nprobe, krefine in [(10, 16, 10), (10, 48, 32)]:
+        say("mixed", dict(k=k, nprobe=nprobe, krefine=krefine))
+        before = res.ivfpq_table_queries()
+        ids, d = ix.search(q, k, nprobe, krefine)
+        say("handed off", res.ivfpq_table_queries() - before, "of", len(q))
+        oids, od = orc.search(q, k, nprobe, krefine)
+        assert_results_match(ids, d, oids, od, label=f"mixed k{k} p{nprobe}")
+        assert np.array_equal(_bits(d), _bits(od)), f"mixed k{k} p{nprobe}"
+    ix.close()

@@ -1,13 +1,15 @@
 """The matrix-core coarse probe (ovvs_amd/csrc/probe.hip) against the oracle.
 
-Searches with dim <= 128, nprobe <= 256 and at least 2 * nprobe groups of
-centroids take the fused probe: approximate fp32 matrix-core scores, a proven
-candidate bound, exact re-score of the candidates. Everything else takes the
-exact score-matrix route. These cases sit in the fused regime (padded dims,
-nlist not a multiple of 16, the largest nprobe) and require results bit-identical
-to the oracle's, including queries whose candidates exceed the re-score capacity
-(tied centroids) and so go through the exact fallback in the same batch as
-ordinary queries.
+Searches with dim <= 1024, nprobe <= 256 and at least 2 * nprobe groups of
+centroids take the fused probe: approximate scores from one bf16 matrix-core
+product of centred operands, a proven candidate bound, exact re-score of the
+candidates. Everything else takes the exact score-matrix route. These cases sit
+in the fused regime (padded dims, dims held in registers and dims read from LDS
+per k-step, nlist not a multiple of 16, the largest nprobe, integer data far from
+the origin, data whose bf16 roundings all err the same way) and require results
+bit-identical to the oracle's, including queries whose candidates exceed the
+re-score capacity (tied centroids) and so go through the exact fallback in the
+same batch as ordinary queries.
 """
 
 from __future__ import annotations
@@ -56,6 +58,8 @@ def _check(ix, orc, q, k, nprobe, krefine, label):
     (40, 10, 1000, (16, 64)),
     (128, 32, 2048, (64, 256)),
     (8, 4, 700, (8, 40)),
+    (200, 25, 1000, (16, 64)),
+    (768, 96, 2048, (32, 128)),
 ])
 def test_matrix_core_probe_matches_oracle(ovvs, res, tmp_path, dim, pq_m, nlist, nprobes):
     rng = np.random.default_rng(dim * 1000 + nlist)
@@ -111,4 +115,46 @@ def test_probe_fallback_for_tied_centroids(ovvs, res, tmp_path):
     orc = Oracle(read_ipq1(same))
     say("all-identical search")
     _check(ix, orc, q, 10, 16, 64, "all identical")
+    ix.close()
+
+
+def test_probe_integer_data_far_from_origin(ovvs, res, tmp_path):
+    """Integer coordinates in [0, 255] (C3's distribution): the centring keeps the
+    bf16 error relative to the clusters' spread rather than to |x| ~ 1600."""
+    rng = np.random.default_rng(255)
+    dim = 128
+    centers = rng.uniform(0, 255, (512, dim))
+    data = np.clip(np.rint(centers[rng.integers(0, 512, 40000)] + 12.0 *
+                           rng.standard_normal((40000, dim))), 0, 255).astype(np.float32)
+    q = np.clip(np.rint(centers[rng.integers(0, 512, 300)] + 12.0 *
+                        rng.standard_normal((300, dim))), 0, 255).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=2048, pq_m=64, pq_nbits=8, resources=res)
+    p = tmp_path / "int255.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for nprobe in (32, 128, 256):
+        say("int255 search", nprobe)
+        _check(ix, orc, q, 100, nprobe, 100, f"int255 p{nprobe}")
+    ix.close()
+
+
+def test_probe_aligned_bf16_rounding(ovvs, res, tmp_path):
+    """Centroids and queries whose coordinates bf16 rounds the same way (magnitude
+    1 + 3 * 2^-10 rounds down to 1) put the approximate scores as far from the exact
+    ones as the bound allows: the candidate sets must still contain the exact probes."""
+    rng = np.random.default_rng(17)
+    dim, nlist = 64, 1024
+    base = np.float32(1.0 + 3.0 * 2.0 ** -10)
+    signs = np.where(rng.random((64, dim)) < 0.5, 1.0, -1.0)
+    data = (base * signs[rng.integers(0, 64, 20000)] +
+            0.05 * rng.standard_normal((20000, dim))).astype(np.float32)
+    q = (base * signs[rng.integers(0, 64, 300)] +
+         0.05 * rng.standard_normal((300, dim))).astype(np.float32)
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=16, pq_nbits=8, resources=res)
+    p = tmp_path / "aligned.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    for nprobe in (8, 64, 256):
+        say("aligned search", nprobe)
+        _check(ix, orc, q, 10, nprobe, 32, f"aligned p{nprobe}")
     ix.close()

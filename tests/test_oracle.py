@@ -313,3 +313,23 @@ def test_scann_oracle_matches_live_reference(seed, tmp_path):
     ref.scann_destroy(h)
     ref.destroy(inner)
     ref.close()
+
+
+def test_ipq1_stream_reader_matches_file_reader(ref_cases, tmp_path):
+    """The streaming IPQ1 reader (bench.py's C5 parity path: the index serialized
+    into a pipe, the dataset section dropped and replaced by the rows in memory)
+    yields the same index as the file reader."""
+    import io
+
+    from oracle.pyoracle import read_ipq1_stream
+
+    manifest, arrays = ref_cases
+    for case in manifest:
+        raw = arrays[f"{case['name']}/ipq1"].tobytes()
+        p = tmp_path / "c.ipq1"
+        p.write_bytes(raw)
+        a = read_ipq1(p)
+        b = read_ipq1_stream(io.BytesIO(raw), a.dataset.copy())
+        assert b.to_bytes() == raw, case["name"]
+    with pytest.raises(ValueError):
+        read_ipq1_stream(io.BytesIO(raw[:-3]), a.dataset.copy())
