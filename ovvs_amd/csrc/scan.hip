@@ -1233,12 +1233,12 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   }
 }
 
-// Shortlists of up to 128 keys run at 7 waves per SIMD (72 VGPRs): the scan is
-// latency-bound, and measured on C2 this balances occupancy against register
-// spills better than 8 (64 VGPRs) or 6 (80). Longer register lists keep the
-// compiler's own allocation.
+// Shortlists of up to 128 keys run at 6 waves per SIMD (80 VGPRs): the scan is
+// latency-bound, and measured on C2 (scan stage 0.287 ms against 0.301 at 7 waves
+// and 0.296-0.301 at 5) this balances occupancy against register spills best.
+// Longer register lists keep the compiler's own allocation.
 template <int KPL, int FD>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_scan(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   scan_query<KPL, FD>(a, smem);
@@ -1801,8 +1801,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 }
 
-// Workgroups of the full-table launch (each takes handed-off queries in turn).
-constexpr unsigned kTableGrid = 1024;
+// Workgroups of the full-table launch (each takes handed-off queries in turn): two per
+// CU, as many as the table's LDS lets run at once at C2's shape.
+constexpr unsigned kTableGrid = 512;
 
 template <int KPL, int DS>
 hipError_t launch_scan_table(const OvvsScanArgs& a, size_t lds, hipStream_t stream) {
