@@ -113,6 +113,18 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Sum of v over the 64 lanes, in every lane (row shifts within 16 lanes, then row
+// broadcasts; all lanes active).
+__device__ __forceinline__ int wave_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 // bf16 bits of x, rounded to nearest even (NaN stays NaN).
 __host__ __device__ __forceinline__ uint16_t bf16_bits(uint32_t u) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
@@ -136,6 +148,69 @@ __device__ __forceinline__ float next_up(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) == 0) return __uint_as_float(1u);
   return __uint_as_float((u & 0x80000000u) ? u - 1u : u + 1u);
+}
+
+// Left-to-right fp32 sum from +0 of x[t]^2 (kCentred: of (x[t] - m[t])^2), t < d, for
+// rows in LDS that start 16-byte aligned: eight 16-byte reads issued before their
+// terms are added (the sum's order is unchanged).
+template <bool kCentred>
+__device__ __forceinline__ float lds_seq_sumsq(const float* x, const float* m, int d) {
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* m4 = reinterpret_cast<const float4*>(m);
+  const int n4 = d >> 2;
+  float s = 0.f;
+  auto add4 = [&](float4 v, float4 w) {
+    const float e0 = kCentred ? v.x - w.x : v.x, e1 = kCentred ? v.y - w.y : v.y;
+    const float e2 = kCentred ? v.z - w.z : v.z, e3 = kCentred ? v.w - w.w : v.w;
+    s = s + e0 * e0;
+    s = s + e1 * e1;
+    s = s + e2 * e2;
+    s = s + e3 * e3;
+  };
+  int i = 0;
+  for (; i + 8 <= n4; i += 8) {
+    float4 v[8], w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = x4[i + j];
+      w[j] = kCentred ? m4[i + j] : v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) add4(v[j], w[j]);
+  }
+  for (; i < n4; ++i) add4(x4[i], kCentred ? m4[i] : x4[i]);
+  for (int t = 4 * n4; t < d; ++t) {
+    const float e = kCentred ? x[t] - m[t] : x[t];
+    s = s + e * e;
+  }
+  return s;
+}
+
+// seq_dot(q, x, d) for d % 4 == 0, q in LDS and x in global memory, both rows 16-byte
+// aligned: the same left-to-right sum from +0, x read twelve 16-byte vectors at a time
+// with all of a chunk's loads issued before its terms are added.
+__device__ __forceinline__ float seq_dot_chunked(const float* q, const float* __restrict__ x, int d) {
+  constexpr int kChunk = 12;
+  const float4* q4 = reinterpret_cast<const float4*>(q);
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const int n4 = d >> 2;
+  float s = 0.f;
+  for (int i = 0; i < n4; i += kChunk) {
+    float4 v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) v[j] = x4[i + j < n4 ? i + j : n4 - 1];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (i + j < n4) {
+        const float4 w = q4[i + j];
+        s = s + w.x * v[j].x;
+        s = s + w.y * v[j].y;
+        s = s + w.z * v[j].z;
+        s = s + w.w * v[j].w;
+      }
+    }
+  }
+  return s;
 }
 
 // Candidate bound T = t + 2E for one query, rounded up (see the file comment).
@@ -208,6 +283,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     L.qs[i] = (q < p.nq && t < dim) ? p.queries[q * dim + t] : 0.f;
   }
   for (int t = static_cast<int>(threadIdx.x); t < dim; t += kThreads) L.mu[t] = p.cmu[t];
+  // A centroid table of at most 2 MB is read into each XCD's L2 while the queries are
+  // staged: the workgroups of one XCD (workgroup b runs on XCD b % 8) each read a slice,
+  // so that the exact re-score finds its rows there instead of in HBM.
+  {
+    const int64_t n4 = static_cast<int64_t>(p.nlist) * dim / 4;
+    if ((dim & 3) == 0 && n4 * 16 <= (int64_t(2) << 20)) {
+      const int per_xcd = (static_cast<int>(gridDim.x) + 7) / 8;
+      const int64_t slice = (n4 + per_xcd - 1) / per_xcd;
+      const int64_t lo = slice * static_cast<int64_t>(blockIdx.x / 8);
+      const int64_t hi = lo + slice < n4 ? lo + slice : n4;
+      const float4* c4 = reinterpret_cast<const float4*>(p.centroids);
+      for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
+        const float4 v = c4[i];
+        asm volatile("" ::"v"(v.x));
+      }
+    }
+  }
   if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
   if (threadIdx.x == 0) L.flag[0] = 0;
   if (p.zero && blockIdx.x == 0 && threadIdx.x < 8) p.zero[threadIdx.x] = 0;
@@ -218,17 +310,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
   if (threadIdx.x < kRows) {
     const int64_t q = q0 + threadIdx.x;
     const float* r = L.qs + threadIdx.x * dq;
-    float s = 0.f, sc = 0.f;
+    float s = 0.f;
     if (p.qnorm) {
       s = q < p.nq ? p.qnorm[q] : 0.f;
     } else {
-      for (int t = 0; t < dim; ++t) s = s + r[t] * r[t];
+      s = lds_seq_sumsq<false>(r, r, dim);
       if (q < p.nq) p.qnorm_out[q] = s;
     }
-    for (int t = 0; t < dim; ++t) {
-      const float d = r[t] - L.mu[t];
-      sc = sc + d * d;
-    }
+    const float sc = lds_seq_sumsq<true>(r, L.mu, dim);
     L.qn[threadIdx.x] = q < p.nq ? s : 0.f;
     L.qcn[threadIdx.x] = q < p.nq ? sc : 0.f;
   }
@@ -316,11 +405,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
       for (int g = 0; g < kG; ++g) {
         if (t + g < t1 && 16 * (t + g) + col < p.nlist) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float a = cn[g] - 2.f * acc[g][r];
-            bad |= a != a;
-            m[r] = __builtin_fminf(m[r], a);
-          }
+        for (int r = 0; r < 4; ++r) {
+          const float a = cn[g] - 2.f * acc[g][r];
+          bad |= a != a;
+          m[r] = __builtin_fminf(m[r], a);
+        }
         }
       }
     }
@@ -353,14 +442,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
       }
       v[rr] = 0;
     }
+    // Counts in the VALU (per-lane sums, then a DPP sum): every wave of the CU runs
+    // this loop at once, and ballot/popcount counting would queue on the scalar unit.
     for (int b = 31; b >= 0; --b) {
       int cnt[kRowsPerWave];
 #pragma unroll
       for (int rr = 0; rr < kRowsPerWave; ++rr) {
         const uint32_t probe = v[rr] | ((1u << b) - 1u);
-        cnt[rr] = 0;
+        int c = 0;
 #pragma unroll
-        for (int i = 0; i < kMaxChunks / 4; ++i) cnt[rr] += __popcll(__ballot(g[rr][i] <= probe));
+        for (int i = 0; i < kMaxChunks / 4; ++i) c += g[rr][i] <= probe ? 1 : 0;
+        cnt[rr] = wave_sum(c);
       }
 #pragma unroll
       for (int rr = 0; rr < kRowsPerWave; ++rr)
@@ -448,21 +540,68 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     const uint32_t c = static_cast<uint32_t>(*s);
     const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
     const float* qrow = L.qs + row * dq;
-    const float dot = (dim & 3) == 0 ? seq_dot_v4_ahead(qrow, crow, dim) : seq_dot(qrow, crow, dim);
+    const float dot = (dim & 3) == 0 ? seq_dot_chunked(qrow, crow, dim) : seq_dot(qrow, crow, dim);
     *s = make_key((L.qn[row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();
-  for (int f = lane; f < total; f += 64) {
-    int rr = 0;
+  // Ranks. A row of at most kCountRank candidates: each candidate's rank is the number
+  // of smaller keys. A longer row: its keys in registers, the P-th smallest key by a
+  // bit search (keys are distinct: exactly P keys are at most it), those P keys moved
+  // to the front of the row in position order, then ranked among themselves.
+  constexpr int kCountRank = 256;
+  constexpr int kKeysPerLane = OVVS_PROBE_CAP / 64;
 #pragma unroll
-    for (int j = 1; j < kRowsPerWave; ++j) rr += f >= pre[j] ? 1 : 0;
+  for (int rr = 0; rr < kRowsPerWave; ++rr) {
     const int row = kRowsPerWave * wave + rr;
-    const uint64_t* keys = L.slot + row * cap;
-    const uint64_t key = keys[f - pre[rr]];
-    int rank = 0;
-    for (int j = 0; j < cnt[rr]; ++j) rank += keys[j] < key ? 1 : 0;
-    if (rank < p.P) p.probes[(q0 + row) * p.P + rank] = static_cast<int32_t>(key & 0xffffffffu);
-    if (rank == 0 && p.order_keys) p.order_keys[q0 + row] = p.list_rank[key & 0xffffffffu] >> p.key_shift;
+    uint64_t* keys = L.slot + row * cap;
+    int n = cnt[rr];
+    if (n > kCountRank) {
+      uint64_t k[kKeysPerLane];
+#pragma unroll
+      for (int i = 0; i < kKeysPerLane; ++i) {
+        const int f = lane + 64 * i;
+        k[i] = f < n ? keys[f] : ~0ull;
+      }
+      uint64_t v = 0;
+      for (int b = 63; b >= 0; --b) {
+        const uint64_t probe = v | ((1ull << b) - 1ull);
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < kKeysPerLane; ++i) c += __popcll(__ballot(k[i] <= probe));
+        if (c < p.P) v |= 1ull << b;
+      }
+      wave_sync();
+      int base = 0;
+#pragma unroll
+      for (int i = 0; i < kKeysPerLane; ++i) {
+        const bool keep = k[i] <= v;
+        const uint64_t bal = __ballot(keep);
+        if (keep) keys[base + __popcll(bal & ((1ull << lane) - 1ull))] = k[i];
+        base += __popcll(bal);
+      }
+      wave_sync();
+      n = p.P;
+    }
+    for (int f = lane; f < n; f += 64) {
+      const uint64_t key = keys[f];
+      int rank = 0;
+      int j = 0;
+      // Eight keys per step, read 16 bytes at a time (the row starts 16-byte aligned).
+      for (; j + 8 <= n; j += 8) {
+        uint64_t kk[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint4 w = reinterpret_cast<const uint4*>(keys + j)[u];
+          kk[2 * u] = (static_cast<uint64_t>(w.y) << 32) | w.x;
+          kk[2 * u + 1] = (static_cast<uint64_t>(w.w) << 32) | w.z;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rank += kk[u] < key ? 1 : 0;
+      }
+      for (; j < n; ++j) rank += keys[j] < key ? 1 : 0;
+      if (rank < p.P) p.probes[(q0 + row) * p.P + rank] = static_cast<int32_t>(key & 0xffffffffu);
+      if (rank == 0 && p.order_keys) p.order_keys[q0 + row] = p.list_rank[key & 0xffffffffu] >> p.key_shift;
+    }
   }
 }
 
