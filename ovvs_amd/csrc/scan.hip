@@ -1818,6 +1818,227 @@ hipError_t launch_scan_table(const OvvsScanArgs& a, size_t lds, hipStream_t stre
   return hipGetLastError();
 }
 
+// ---- per-wave full scan (handed-off queries whose codebook fits in LDS) ----
+//
+// The same outputs as table_query, for shapes whose whole codebook fits in LDS beside
+// sixteen waves' working areas (C2: 98 KB): one workgroup of sixteen waves per CU
+// copies the codebook into LDS once, then every wave takes handed-off queries in turn
+// and scores every row of every probed list on its own, one row per lane, each entry
+// computed from the LDS codebook where the row uses it (direct_entry: the reference's
+// table arithmetic) and added in subspace order. There is no per-list table build and
+// no barrier after the copy, so sixteen independent waves per CU hide each other's
+// code-load latency.
+constexpr int kWaveScanWaves = 16;
+constexpr int kWaveScanThreads = 64 * kWaveScanWaves;
+// Workgroups of the per-wave launch: one per CU of an MI355X (each holds the codebook).
+constexpr unsigned kWaveScanGrid = 256;
+
+struct WaveScanLayout {
+  size_t cb_off;       // [pq_m][ks][dsub] f32
+  size_t wave_off;     // per wave, wave_stride bytes:
+  size_t wave_stride;  //   query [dim_pad] f32 | residual [dim_pad] f32 | keys [kBufCap] u64 |
+                       //   positions [kBufCap] i32
+  size_t dim_bytes;    // dim_pad * 4, rounded to 16
+  size_t total;
+};
+
+__host__ __device__ inline WaveScanLayout wave_scan_layout(int pq_m, int ks, int dsub, int dim) {
+  WaveScanLayout L;
+  L.cb_off = 0;
+  L.wave_off = round16(static_cast<size_t>(pq_m) * ks * dsub * 4);
+  L.dim_bytes = round16(static_cast<size_t>((dim + 3) & ~3) * 4);
+  L.wave_stride = 2 * L.dim_bytes + static_cast<size_t>(kBufCap) * 12;
+  L.total = L.wave_off + kWaveScanWaves * L.wave_stride;
+  return L;
+}
+
+// The per-wave scan serves shortlists of up to 128 keys, dsub 1, 2, 4 or 8 and dim up
+// to 1024 when its LDS fits a workgroup.
+__host__ __device__ inline bool wave_scan_ok(int pq_m, int ks, int dsub, int dim, int K) {
+  return K <= 128 && (dsub == 1 || dsub == 2 || dsub == 4 || dsub == 8) && dim <= kTableMaxDim &&
+         wave_scan_layout(pq_m, ks, dsub, dim).total <= 160u * 1024u;
+}
+
+template <int KPL, int DS>
+__device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, const float* cb,
+                                           unsigned char* area, size_t dim_bytes) {
+  const int lane = lane_id();
+  float* qs = reinterpret_cast<float*>(area);
+  float* resid = reinterpret_cast<float*>(area + dim_bytes);
+  uint64_t* bufk = reinterpret_cast<uint64_t*>(area + 2 * dim_bytes);
+  int32_t* bufp = reinterpret_cast<int32_t*>(area + 2 * dim_bytes + static_cast<size_t>(kBufCap) * 8);
+  const int K = a.K, P = a.P, pq_m = a.pq_m, dim = a.dim, ks = a.ks;
+  const int nblocks = (pq_m + kBlock - 1) / kBlock;
+  const uint32_t tile_bytes = static_cast<uint32_t>(nblocks) * kTile * kBlock;
+
+  for (int t = lane; t < dim; t += 64) qs[t] = a.queries[q * dim + t];
+  uint64_t lk[KPL];
+  int32_t lp[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    lk[j] = kNoKey;
+    lp[j] = -1;
+  }
+  uint64_t thr = kNoKey;  // the wave's K-th key
+  int cnt = 0;
+  uint32_t ord_base = 0;
+  auto flush = [&]() {
+    const int take = cnt < 64 ? cnt : 64;
+    uint64_t bk = lane < take ? bufk[lane] : kNoKey;
+    int32_t bp = lane < take ? bufp[lane] : -1;
+    const int rest = cnt - take;
+    if (lane < rest) {
+      const uint64_t mk = bufk[64 + lane];
+      const int32_t mp = bufp[64 + lane];
+      bufk[lane] = mk;
+      bufp[lane] = mp;
+    }
+    cnt = rest;
+    sort64(bk, bp);
+    merge64<KPL>(lk, lp, bk, bp);
+    thr = kth_key<KPL>(lk, K);
+  };
+  auto offer = [&](bool ok, float score, int32_t pos, int32_t ord) {
+    uint64_t key = kNoKey;
+    if (ok) key = make_key(score, ord_base + static_cast<uint32_t>(ord));
+    const bool pass = key < thr;
+    const uint64_t bal = __ballot(pass);
+    if (bal) {
+      const int before = __popcll(bal & ((1ull << lane) - 1ull));
+      if (pass) {
+        bufk[cnt + before] = key;
+        bufp[cnt + before] = pos;
+      }
+      cnt += __popcll(bal);
+      if (cnt >= 64) flush();
+    }
+  };
+
+  int32_t rows_total = 0, lists = 0, bad = 0;
+  uint32_t ord = 0;
+  for (int p = 0; p < P; ++p) {
+    const int l = a.probes[q * P + p];
+    if (static_cast<uint32_t>(l) >= static_cast<uint32_t>(a.nlist)) {
+      bad = 1;
+      continue;
+    }
+    const int32_t rows = static_cast<int32_t>(a.list_offsets[l + 1] - a.list_offsets[l]);
+    if (rows == 0) continue;
+    rows_total += rows;
+    ++lists;
+    ord_base = ord;
+    ord += static_cast<uint32_t>(rows);
+    const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * dim;
+    for (int t = lane; t < dim; t += 64) resid[t] = qs[t] - cv[t];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int s1 = a.list_seg[l + 1];
+    for (int sg = a.list_seg[l]; sg < s1; ++sg) {
+      const int32_t st = a.seg_start[sg];
+      const int32_t len = a.seg_len[sg];
+      for (int32_t t0 = 0; t0 < len; t0 += kTile) {
+        const int32_t pos = st + t0 + lane;
+        bool ok = lane < len - t0;
+        const int32_t at = ok ? pos : st;
+        if (ok && a.bitset) {
+          const int64_t id = a.ids[pos];
+          ok = ((a.bitset[id >> 3] >> (id & 7)) & 1u) != 0;
+        }
+        const int32_t rord = a.rord[at];
+        const unsigned char* __restrict__ cbp =
+            a.codes + static_cast<size_t>(at >> 6) * tile_bytes + (at & (kTile - 1)) * kBlock;
+        float sc = 0.f;
+        for (int b0 = 0; b0 < nblocks; b0 += kPfBlocks) {
+          uint2 w[kPfBlocks];
+#pragma unroll
+          for (int i = 0; i < kPfBlocks; ++i)
+            w[i] = *reinterpret_cast<const uint2*>(cbp + (b0 + i < nblocks ? b0 + i : nblocks - 1) * (kTile * kBlock));
+#pragma unroll
+          for (int i = 0; i < kPfBlocks; ++i) {
+            const int m0 = (b0 + i) * kBlock;
+            if (m0 >= pq_m) break;
+            const int mb = pq_m - m0 < kBlock ? pq_m - m0 : kBlock;
+            const uint32_t wv[2] = {w[i].x, w[i].y};
+            if (mb == kBlock) {
+              float v[kBlock];
+#pragma unroll
+              for (int j = 0; j < kBlock; ++j) {
+                const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                v[j] = direct_entry<DS>(resid, cb, m0 + j, code, ks, DS);
+              }
+#pragma unroll
+              for (int j = 0; j < kBlock; ++j) sc = sc + v[j];
+            } else {
+              for (int j = 0; j < mb; ++j) {
+                const int code = static_cast<int>((wv[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                sc = sc + direct_entry<DS>(resid, cb, m0 + j, code, ks, DS);
+              }
+            }
+          }
+        }
+        offer(ok, sc, pos, rord);
+      }
+    }
+  }
+  if (cnt > 0 && cnt <= 8) {
+    for (int t = 0; t < cnt; ++t) insert_one<KPL>(lk, lp, bufk[t], bufp[t]);
+    cnt = 0;
+  } else {
+    while (cnt > 0) flush();
+  }
+  int valid = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int e = j * 64 + lane;
+    if (e < K) {
+      a.out_keys[q * K + e] = lk[j];
+      a.out_pos[q * K + e] = lp[j];
+      valid += lk[j] != kNoKey;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
+  if (lane == 0) {
+    a.out_count[q] = valid;
+    a.out_stats[q * 4 + 0] = rows_total;
+    a.out_stats[q * 4 + 1] = lists;
+    a.out_stats[q * 4 + 2] = valid;
+    a.out_stats[q * 4 + 3] = bad;
+  }
+}
+
+template <int KPL, int DS>
+__global__ __launch_bounds__(kWaveScanThreads) void k_scan_wave(const OvvsScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const unsigned int n = *a.punt_count;
+  if (blockIdx.x * kWaveScanWaves >= n) return;  // no query for any wave here
+  const WaveScanLayout L = wave_scan_layout(a.pq_m, a.ks, DS, a.dim);
+  float* cb = reinterpret_cast<float*>(smem + L.cb_off);
+  const int n4 = a.pq_m * a.ks * DS / 4;  // ks >= 16: a whole number of 16-byte vectors
+  const float4* src = reinterpret_cast<const float4*>(a.codebooks);
+  for (int i = static_cast<int>(threadIdx.x); i < n4; i += kWaveScanThreads)
+    reinterpret_cast<float4*>(cb)[i] = src[i];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  unsigned char* area = smem + L.wave_off + static_cast<size_t>(wave) * L.wave_stride;
+  for (unsigned int i = blockIdx.x * kWaveScanWaves + wave; i < n; i += gridDim.x * kWaveScanWaves)
+    wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes);
+}
+
+template <int KPL, int DS>
+hipError_t launch_scan_wave(const OvvsScanArgs& a, hipStream_t stream) {
+  const size_t lds = wave_scan_layout(a.pq_m, a.ks, DS, a.dim).total;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_scan_wave<KPL, DS>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_scan_wave<KPL, DS>), dim3(kWaveScanGrid), dim3(kWaveScanThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
 int kpl_for(int K) { return K <= 64 ? 1 : K <= 128 ? 2 : K <= 256 ? 4 : K <= 512 ? 8 : 16; }
 
 }  // namespace
@@ -1882,6 +2103,18 @@ extern "C" hipError_t ovvs_hip_scan_table(const OvvsScanArgs* args, hipStream_t 
   const size_t lds = ovvs_hip_scan_table_lds_bytes(a.pq_m, a.ks, a.dim, a.K, a.P);
   if (lds == 0) return hipErrorInvalidValue;
   const int kpl = kpl_for(a.K);
+  if (wave_scan_ok(a.pq_m, a.ks, a.dsub, a.dim, a.K)) {
+    switch (a.dsub * 4 + kpl) {
+      case 1 * 4 + 1: return launch_scan_wave<1, 1>(a, stream);
+      case 2 * 4 + 1: return launch_scan_wave<1, 2>(a, stream);
+      case 4 * 4 + 1: return launch_scan_wave<1, 4>(a, stream);
+      case 8 * 4 + 1: return launch_scan_wave<1, 8>(a, stream);
+      case 1 * 4 + 2: return launch_scan_wave<2, 1>(a, stream);
+      case 2 * 4 + 2: return launch_scan_wave<2, 2>(a, stream);
+      case 4 * 4 + 2: return launch_scan_wave<2, 4>(a, stream);
+      default: return launch_scan_wave<2, 8>(a, stream);
+    }
+  }
   if (kpl <= 2 && table_cb_in_regs(a.pq_m, a.ks, a.dsub)) {
     switch (a.dsub * 4 + kpl) {
       case 1 * 4 + 1: return launch_scan_table<1, 1>(a, lds, stream);

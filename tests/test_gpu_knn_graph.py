@@ -101,3 +101,33 @@ def test_knn_graph_matches_reference_call_sequence(ovvs, res, case):
     ref.destroy(h)
     ref.close()
     assert np.array_equal(g, assemble(np.stack(rows), degree))
+
+
+def test_knn_graph_spans_search_batches(ovvs, res, tmp_path):
+    """70,000 rows: the graph's searches run in batches of 65,536 rows
+    (knn_graph_index.cpp), so the second batch's query offsets into the device rows,
+    its self-exclusion (row ids from 65,536 on) and the reuse of the workspace across
+    batches are exercised. Rows around the batch boundary, the last rows and a random
+    sample are checked against the oracle's search over the index libovvs builds."""
+    n, dim, degree = 70_000, 8, 8
+    rng = np.random.default_rng(70)
+    c = rng.standard_normal((64, dim)).astype(np.float32)
+    x = (c[rng.integers(0, 64, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    nlist, pq_m = shape_params(n, dim)
+    say("knn graph across batches", n, dim, degree, nlist, pq_m)
+    g = ovvs.neighbors.ivf_pq.knn_graph(x, degree, metric=0, resources=res)
+    assert g.shape == (n, degree)
+    ix = ovvs.neighbors.ivf_pq.build(x, metric=0, nlist=nlist, pq_m=pq_m, pq_nbits=8,
+                                     resources=res)
+    p = tmp_path / "knn_batches.ipq1"
+    ix.serialize(p)
+    ix.close()
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.arange(65_516, 65_556),
+                                     np.arange(n - 20, n), rng.integers(0, n, 300)]))
+    say("oracle search of", len(rows), "rows")
+    ids, _ = Oracle(read_ipq1(p)).search(x[rows], degree + 1, nlist, degree + 1)
+    for r, row in zip(rows, ids):
+        kept = [int(v) for v in row if v != r and v >= 0][:degree]
+        want = np.full(degree, -1, dtype=np.int32)
+        want[:len(kept)] = kept
+        assert np.array_equal(g[r], want), f"row {r}"
