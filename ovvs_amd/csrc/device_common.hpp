@@ -70,6 +70,34 @@ __device__ __forceinline__ float seq_dot_v4(const float* __restrict__ q,
   return s;
 }
 
+// seq_dot(q, x, d) for d % 4 == 0 with both rows 16-byte aligned (q typically in LDS,
+// x a row in global memory): the same left-to-right sum from +0, x read twelve 16-byte
+// vectors at a time with all of a chunk's loads issued before its terms are added, so
+// that a row costs a few memory round trips instead of one per four vectors.
+__device__ __forceinline__ float seq_dot_v4_chunked(const float* q, const float* __restrict__ x, int d) {
+  constexpr int kChunk = 12;
+  const float4* q4 = reinterpret_cast<const float4*>(q);
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const int n4 = d >> 2;
+  float s = 0.f;
+  for (int i = 0; i < n4; i += kChunk) {
+    float4 v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) v[j] = x4[i + j < n4 ? i + j : n4 - 1];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (i + j < n4) {
+        const float4 w = q4[i + j];
+        s = s + w.x * v[j].x;
+        s = s + w.y * v[j].y;
+        s = s + w.z * v[j].z;
+        s = s + w.w * v[j].w;
+      }
+    }
+  }
+  return s;
+}
+
 // seq_dot_v4 with the row x (global memory) double-buffered: the next four
 // vectors are requested before the current four are summed, so one memory round
 // trip overlaps the next. q is read from LDS as it is consumed. Same sum, same

@@ -186,33 +186,6 @@ __device__ __forceinline__ float lds_seq_sumsq(const float* x, const float* m, i
   return s;
 }
 
-// seq_dot(q, x, d) for d % 4 == 0, q in LDS and x in global memory, both rows 16-byte
-// aligned: the same left-to-right sum from +0, x read twelve 16-byte vectors at a time
-// with all of a chunk's loads issued before its terms are added.
-__device__ __forceinline__ float seq_dot_chunked(const float* q, const float* __restrict__ x, int d) {
-  constexpr int kChunk = 12;
-  const float4* q4 = reinterpret_cast<const float4*>(q);
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  const int n4 = d >> 2;
-  float s = 0.f;
-  for (int i = 0; i < n4; i += kChunk) {
-    float4 v[kChunk];
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) v[j] = x4[i + j < n4 ? i + j : n4 - 1];
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      if (i + j < n4) {
-        const float4 w = q4[i + j];
-        s = s + w.x * v[j].x;
-        s = s + w.y * v[j].y;
-        s = s + w.z * v[j].z;
-        s = s + w.w * v[j].w;
-      }
-    }
-  }
-  return s;
-}
-
 // Candidate bound T = t + 2E for one query, rounded up (see the file comment).
 // qn: the query's exact squared norm (sequential fp32 sum), qcn: the sequential
 // fp32 sum of its squared centred coordinates, cn_max / ccn_max: the largest of the
@@ -540,7 +513,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     const uint32_t c = static_cast<uint32_t>(*s);
     const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
     const float* qrow = L.qs + row * dq;
-    const float dot = (dim & 3) == 0 ? seq_dot_chunked(qrow, crow, dim) : seq_dot(qrow, crow, dim);
+    const float dot = (dim & 3) == 0 ? seq_dot_v4_chunked(qrow, crow, dim) : seq_dot(qrow, crow, dim);
     *s = make_key((L.qn[row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();
