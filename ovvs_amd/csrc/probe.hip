@@ -256,23 +256,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     L.qs[i] = (q < p.nq && t < dim) ? p.queries[q * dim + t] : 0.f;
   }
   for (int t = static_cast<int>(threadIdx.x); t < dim; t += kThreads) L.mu[t] = p.cmu[t];
-  // A centroid table of at most 2 MB is read into each XCD's L2 while the queries are
-  // staged: the workgroups of one XCD (workgroup b runs on XCD b % 8) each read a slice,
-  // so that the exact re-score finds its rows there instead of in HBM.
-  {
-    const int64_t n4 = static_cast<int64_t>(p.nlist) * dim / 4;
-    if ((dim & 3) == 0 && n4 * 16 <= (int64_t(2) << 20)) {
-      const int per_xcd = (static_cast<int>(gridDim.x) + 7) / 8;
-      const int64_t slice = (n4 + per_xcd - 1) / per_xcd;
-      const int64_t lo = slice * static_cast<int64_t>(blockIdx.x / 8);
-      const int64_t hi = lo + slice < n4 ? lo + slice : n4;
-      const float4* c4 = reinterpret_cast<const float4*>(p.centroids);
-      for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
-        const float4 v = c4[i];
-        asm volatile("" ::"v"(v.x));
-      }
-    }
-  }
   if (threadIdx.x < kRows) L.count[threadIdx.x] = 0;
   if (threadIdx.x == 0) L.flag[0] = 0;
   if (p.zero && blockIdx.x == 0 && threadIdx.x < 8) p.zero[threadIdx.x] = 0;
