@@ -173,11 +173,13 @@ struct OvvsScanArgs {
 // Code scan + per-query shortlist of the K best (ADC score, dense ordinal) rows
 // over all probed lists.
 hipError_t ovvs_hip_scan(const OvvsScanArgs* args, hipStream_t stream);
-// Full-table scan of the queries ovvs_hip_scan handed off (punt[0 .. *punt_count)):
-// for every probed list, a lookup table of every subspace built in LDS, every row of
-// the list scored; the same outputs (out_keys, out_pos, out_count, out_stats) as
-// ovvs_hip_scan, bit for bit. A fixed number of workgroups take the handed-off
-// queries in turn (a search without any returns at once).
+// Full scan of the queries ovvs_hip_scan handed off (punt[0 .. *punt_count)): every
+// row of every probed list scored, with the same outputs (out_keys, out_pos,
+// out_count, out_stats) as ovvs_hip_scan, bit for bit. When the codebook fits in LDS
+// beside sixteen waves (dsub 1, 2, 4 or 8, K <= 128), one query per wave computes the
+// entries each row uses from it; otherwise each list's whole table is built in LDS.
+// A fixed number of workgroups take the handed-off queries in turn (a search without
+// any returns at once).
 hipError_t ovvs_hip_scan_table(const OvvsScanArgs* args, hipStream_t stream);
 // Dynamic LDS bytes of the full-table scan (0 if it does not fit the 160 KiB of a
 // gfx950 workgroup, the table holding pq_m * ks fp32 entries, or if dim > 1024 or

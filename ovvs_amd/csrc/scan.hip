@@ -39,6 +39,10 @@
 //     threshold it publishes in LDS: rows are appended with ballot/popcount (no
 //     atomics), buffers are merged by a cross-lane bitonic sort plus a bitonic
 //     merge, and at the end the four lists are merged once.
+//   * Data without cluster structure defeats the bounds: a query whose rows scored
+//     after the first phase exceed a budget stops and is handed off to a full
+//     scan (k_scan_wave: the codebook in LDS, one query per wave; k_scan_table:
+//     each list's whole table in LDS), which rewrites all of its outputs.
 // Keys are (order-preserving score bits << 32 | raw ordinal); a row's raw ordinal
 // is the number of rows of earlier probed lists plus its index within its list,
 // which orders accepted rows exactly as the dense ordinal does, whatever order the
