@@ -527,8 +527,10 @@ def test_table_mode_unclustered_and_mixed_against_oracle(ovvs, res, tmp_path):
     ix.serialize(p)
     orc = Oracle(read_ipq1(p))
     bitset = np.packbits((rng.random(40000) < 0.5).astype(np.uint8), bitorder="little")
+    # Shortlists of 10, 64 and 128 keys take the per-wave scan (codebook in LDS), 129 and
+    # 300 the whole-table scan.
     for k, nprobe, krefine, bits in [(10, 16, 10, None), (10, 32, 64, bitset), (100, 8, 300, None),
-                                     (1, 64, 1, None)]:
+                                     (1, 64, 1, None), (10, 16, 128, bitset), (10, 16, 129, None)]:
         say("iso", dict(k=k, nprobe=nprobe, krefine=krefine, bitset=bits is not None))
         before = res.ivfpq_table_queries()
         ids, d = ix.search(q_iso, k, nprobe, krefine, bitset=bits)
