@@ -216,6 +216,20 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // staged and copied only after the search has succeeded.
     int64_t* d_oid = device_io ? neighbors : cv.take<int64_t>(nqk);
     float* d_odist = device_io ? distances : cv.take<float>(nqk);
+    // Host outputs: the refine kernel writes straight into the pinned staging buffer
+    // (mapped into the device's address space), which replaces two device-to-host
+    // copies; they reach the caller's arrays only after the checks below.
+    bool direct_out = false;
+    if (io == Io::kHost) {
+      void* pdev = nullptr;
+      if (hipHostGetDevicePointer(&pdev, res->pinned, 0) == hipSuccess && pdev) {
+        d_oid = reinterpret_cast<int64_t*>(static_cast<unsigned char*>(pdev) + pin_ids);
+        d_odist = reinterpret_cast<float*>(static_cast<unsigned char*>(pdev) + pin_dist);
+        direct_out = true;
+      } else {
+        (void)hipGetLastError();
+      }
+    }
     // counters: [0] candidate rows, [1] non-empty probed lists, [2] shortlist entries,
     // [3] out-of-range probe ids or shortlist positions, [4] queries handed off to the
     // full-table scan (as unsigned int); [5, 8) unused.
@@ -376,7 +390,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
     ovvs::saturating_add(work.d2h_calls, 1);
     ovvs::saturating_add(work.d2h_bytes, 40);
-    if (!device_io) {
+    if (!device_io && !direct_out) {
       SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
       SEARCH_HIP(hipMemcpyAsync(pin + pin_dist, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));
       ovvs::saturating_add(work.d2h_calls, 2);
