@@ -373,8 +373,8 @@ __device__ __forceinline__ float group_sum(float e, int gl) {
   if (gl >= 2) e = e + dpp_f<0x4E>(e);   // quad_perm(2, 3, 0, 1): lane ^ 2
   if (gl >= 3) e = e + dpp_f<0x141>(e);  // row_half_mirror: the other quad of 8 lanes
   if (gl >= 4) e = e + dpp_f<0x140>(e);  // row_mirror: the other half of 16 lanes
-  if (gl >= 5) e = e + __shfl_xor(e, 16, 64);
-  if (gl >= 6) e = e + __shfl_xor(e, 32, 64);
+  if (gl >= 5) e = e + __uint_as_float(xor_lane(__float_as_uint(e), 16));
+  if (gl >= 6) e = e + __uint_as_float(xor_lane(__float_as_uint(e), 32));
   return e;
 }
 
@@ -526,9 +526,10 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     const float v = __builtin_fabsf(qs[t]);
     qmax = (v <= qmax) ? qmax : v;  // NaN propagates
   }
+  // Lane exchanges as DPP and row swaps (no lane-address registers to keep live).
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
-    const float v = __shfl_xor(qmax, o, 64);
+    const float v = __uint_as_float(xor_lane(__float_as_uint(qmax), o));
     qmax = (v <= qmax) ? qmax : v;
   }
   const float slack = 0x1p-21f * (qmax + a.box_cmax);
@@ -1005,7 +1006,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     if (t < a.P && t_rows[t] > 0 && !(lboxes && t_lbound[t] > thr_hi)) n = t_ngrp[t];
     int32_t live = n > 0 ? t_rows[t] : 0;  // rows of the lists whose bound passed
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) live += __shfl_xor(live, o, 64);
+    for (int o = 32; o >= 1; o >>= 1) live += static_cast<int32_t>(xor_lane(static_cast<uint32_t>(live), o));
     if (lane == 0) atomicAdd(&misc[9], live);
     const int32_t incl = wave_incl_scan(n);
     if (t < a.P) {
@@ -1222,7 +1223,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) valid += __shfl_xor(valid, o, 64);
+    for (int o = 32; o >= 1; o >>= 1) valid += static_cast<int>(xor_lane(static_cast<uint32_t>(valid), o));
     if (lane == 0 && misc[8] > budget) a.punt[atomicAdd(a.punt_count, 1u)] = static_cast<int32_t>(q);
     if (lane == 0) {
       a.out_count[q] = valid;
