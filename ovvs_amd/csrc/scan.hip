@@ -99,6 +99,9 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int s) {
   }
 }
 
+// v of the previous lane (lane 0: lane 63's), DPP wave_ror:1. All lanes active.
+__device__ __forceinline__ uint32_t wave_ror1(uint32_t v) { return dpp_u<0x13C>(v); }
+
 // v of lane 63 - this lane (row_mirror reverses each 16-lane row, then the rows swap).
 __device__ __forceinline__ uint32_t rev_lane(uint32_t v) {
   return xor_lane(xor_lane(dpp_u<0x140>(v), 16), 32);
@@ -199,11 +202,15 @@ __device__ __forceinline__ void insert_one(uint64_t (&lk)[KPL], int32_t (&lp)[KP
   int32_t prev_tail_p = 0;
 #pragma unroll
   for (int j = 0; j < KPL; ++j) {
-    // Element e = j*64 + lane takes element e-1 when e > at.
-    uint64_t up = shfl_u64(lk[j], (lane + 63) & 63);
-    int32_t upp = __shfl(lp[j], (lane + 63) & 63, 64);
-    const uint64_t tail = shfl_u64(lk[j], 63);
-    const int32_t tailp = __shfl(lp[j], 63, 64);
+    // Element e = j*64 + lane takes element e-1 when e > at: the previous lane's
+    // element by a wave rotation (DPP wave_ror:1), lane 63's by readlane.
+    uint64_t up = (static_cast<uint64_t>(wave_ror1(static_cast<uint32_t>(lk[j] >> 32))) << 32) |
+                  wave_ror1(static_cast<uint32_t>(lk[j]));
+    int32_t upp = static_cast<int32_t>(wave_ror1(static_cast<uint32_t>(lp[j])));
+    const uint64_t tail =
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lk[j] >> 32), 63))) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lk[j]), 63));
+    const int32_t tailp = __builtin_amdgcn_readlane(lp[j], 63);
     if (lane == 0) {
       up = prev_tail;
       upp = prev_tail_p;
@@ -805,9 +812,12 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
       }
     }
-    for (int o = 1; o < G; o <<= 1) {
-      e0 = e0 + __shfl_xor(e0, o, 64);
-      et = et + __shfl_xor(et, o, 64);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      if (o < G) {
+        e0 = e0 + __uint_as_float(xor_lane(__float_as_uint(e0), o));
+        et = et + __uint_as_float(xor_lane(__float_as_uint(et), o));
+      }
     }
   };
 
