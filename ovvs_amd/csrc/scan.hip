@@ -1248,12 +1248,13 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   }
 }
 
-// Shortlists of up to 128 keys run at 6 waves per SIMD (80 VGPRs): the scan is
-// latency-bound, and measured on C2 (scan stage 0.287 ms against 0.301 at 7 waves
-// and 0.296-0.301 at 5) this balances occupancy against register spills best.
-// Longer register lists keep the compiler's own allocation.
+// Shortlists of up to 64 keys run at 6 waves per SIMD (80 VGPRs, no spills), those of
+// up to 128 at 7 (72 VGPRs): the scan is latency-bound, and measured on C2 (64 keys)
+// 6 waves were within 1% of 7 without 7's spill traffic, and on C3 (128 keys) 7
+// waves took 1.24-1.25 ms against 1.31 at 6. Longer register lists keep the
+// compiler's own allocation.
 template <int KPL, int FD>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_scan(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KPL == 1 ? 6 : 7))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   scan_query<KPL, FD>(a, smem);
