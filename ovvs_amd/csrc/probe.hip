@@ -344,12 +344,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     }
   };
 
+  // A wave takes the chunks wave, wave + kWaves, ..., starting at a rotation that
+  // differs between neighbouring workgroups of an XCD (blockIdx.x / 8), so that they
+  // do not all miss in L2 on the same tiles at the same time.
+  const int nmine = (nch - wave + kWaves - 1) / kWaves;
+  const int rot = nmine > 0 ? static_cast<int>((blockIdx.x >> 3) % static_cast<uint32_t>(nmine)) : 0;
+  auto chunk_of = [&](int i) {
+    const int j = i + rot;
+    return wave + kWaves * (j >= nmine ? j - nmine : j);
+  };
+
   // Pass 1: running minimum of a' over each (chunk, column) group, and of each
   // query row over the chunk. A NaN score (only non-finite inputs make one) turns
   // chunk skipping off for the workgroup.
   const int ng = 16 * nch;
   bool bad = false;
-  for (int ch = wave; ch < nch; ch += kWaves) {
+  for (int i = 0; i < nmine; ++i) {
+    const int ch = chunk_of(i);
     const int t0 = ch * shape.gt;
     const int t1 = min(t0 + shape.gt, shape.ntile);
     float m[4] = {__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff()};
@@ -438,7 +449,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
   }
   const bool may_skip = L.flag[0] == 0;
   const int cap = shape.cap;
-  for (int ch = wave; ch < nch; ch += kWaves) {
+  for (int i = 0; i < nmine; ++i) {
+    const int ch = chunk_of(i);
     if (may_skip) {
       bool hit = false;
 #pragma unroll
@@ -451,19 +463,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
       f32x4 acc[kG];
       float cn[kG];
       batch(t, t1, acc, cn);
+      // Per tile, bit r: the lane's centroid is a candidate of its row r; the
+      // candidates are appended one per lane and step.
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
         const int c = 16 * (t + g) + col;
+        uint32_t hits = 0;
         if (t + g < t1 && c < p.nlist) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float a = cn[g] - 2.f * acc[g][r];
-            if (!(a > T[r])) {
-              const int row = 4 * (lane >> 4) + r;
-              const int at = atomicAdd(&L.count[row], 1);
-              if (at < cap) L.slot[row * cap + at] = static_cast<uint64_t>(c);
-            }
-          }
+          for (int r = 0; r < 4; ++r) hits |= !(cn[g] - 2.f * acc[g][r] > T[r]) ? 1u << r : 0u;
+        }
+        while (hits) {
+          const int row = 4 * (lane >> 4) + __builtin_ctz(hits);
+          hits &= hits - 1u;
+          const int at = atomicAdd(&L.count[row], 1);
+          if (at < cap) L.slot[row * cap + at] = static_cast<uint64_t>(c);
         }
       }
     }
