@@ -14,7 +14,8 @@
 // read 16 bytes at a time when dim % 4 == 0), the (key, rank) pairs are sorted in
 // LDS by a single-wave bitonic network, and the first k slots are written. LDS is
 // sized to the shortlist (a power of two >= krefine), so short shortlists keep
-// many waves resident.
+// many waves resident. Longer shortlists with dim % 4 == 0 stage their rows through
+// LDS in chunks read by whole-row 16-byte loads (k_refine_staged).
 #include <algorithm>
 
 #include "device_common.hpp"
@@ -102,6 +103,42 @@ __device__ void refine_stats(const OvvsRefineArgs& a, int64_t g, int64_t ng) {
   }
 }
 
+// Sorts the M keys in LDS (one wave's bitonic network) and writes the first k
+// outputs of query q: (id, distance) of the smallest keys, (-1, +inf) past cnt.
+// The id of entry i is lid[i] when lid is given, else looked up again.
+__device__ void sort_and_publish(const OvvsRefineArgs& a, int64_t q, uint64_t* keys,
+                                 const float* vals, int M, int cnt, const int64_t* lid) {
+  const int lane = threadIdx.x;
+  __syncthreads();
+  for (int k = 2; k <= M; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = lane; i < M; i += 64) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint64_t x = keys[i], y = keys[p];
+          if ((x > y) == ((i & k) == 0)) {
+            keys[i] = y;
+            keys[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int64_t kk = a.k < cnt ? a.k : cnt;
+  for (int64_t t = lane; t < a.k; t += 64) {
+    int64_t id = -1;
+    float d = __builtin_inff();
+    if (t < kk && keys[t] != kNoKey) {
+      const int i = static_cast<int>(keys[t] & 0xffffffffu);
+      id = lid ? lid[i] : a.ids[a.short_pos[q * a.K + i]];
+      d = a.metric == kIP ? -vals[i] : vals[i];
+    }
+    a.out_ids[q * a.k + t] = id;
+    a.out_dist[q * a.k + t] = d;
+  }
+}
+
 __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
   if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
     refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
@@ -139,34 +176,112 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax)
     }
     keys[i] = key;
   }
+  sort_and_publish(a, q, keys, vals, M, cnt, nullptr);
+}
+
+// Shortlists longer than 16 with dim % 4 == 0 (dim <= 4 * kStageVecMax): the rows
+// of R entries at a time are read by the whole wave, consecutive lanes taking
+// consecutive 16-byte vectors of a row (a load instruction covers whole rows instead
+// of 64 scattered vectors), kStageLoads loads in flight per lane, into LDS rows
+// padded by 16 bytes; each lane then scores its own entry from LDS with the same
+// metric_value, so the sums and their order are those of k_refine.
+constexpr int kStageRowsMax = 64;
+constexpr int kStageLoads = 8;
+constexpr size_t kStageBytes = 16 * 1024;
+constexpr int kStageVecMax = 255;
+
+// LDS: query row [dim] f32 | keys [M] u64 | vals [M] f32 | ids of the entries [M]
+// i64 | rows [R * stride] f32.
+struct StagedCarve {
+  size_t keys_off, vals_off, rid_off, rows_off, lds;
+};
+
+__host__ __device__ inline StagedCarve staged_carve(int dim, int M, int R, int stride) {
+  StagedCarve c;
+  c.keys_off = align16(static_cast<size_t>(dim) * 4);
+  c.vals_off = c.keys_off + static_cast<size_t>(M) * 8;
+  c.rid_off = align16(c.vals_off + static_cast<size_t>(M) * 4);
+  c.rows_off = align16(c.rid_off + static_cast<size_t>(M) * 8);
+  c.lds = c.rows_off + static_cast<size_t>(R) * stride * 4;
+  return c;
+}
+
+__global__ __launch_bounds__(64) void k_refine_staged(const OvvsRefineArgs a, int Mmax, int R,
+                                                      int stride) {
+  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
+    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
+    return;
+  }
+  extern __shared__ __align__(16) unsigned char smem[];
+  const StagedCarve L = staged_carve(a.dim, Mmax, R, stride);
+  float* qs = reinterpret_cast<float*>(smem);
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem + L.keys_off);
+  float* vals = reinterpret_cast<float*>(smem + L.vals_off);
+  int64_t* rid = reinterpret_cast<int64_t*>(smem + L.rid_off);
+  float* rows = reinterpret_cast<float*>(smem + L.rows_off);
+  const int64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int t = lane; t < a.dim; t += 64) qs[t] = a.queries[q * a.dim + t];
+  int cnt = a.short_count[q];
+  cnt = cnt < 0 ? 0 : (cnt > a.K ? a.K : cnt);
+  int M = 1;
+  while (M < cnt) M <<= 1;
+  // Vector j = lane + 64 i of a chunk is vector j % nv of its row j / nv; the lane
+  // steps (de, dv) per 64.
+  const int nv = a.dim >> 2;
+  const int de = 64 / nv, dv = 64 - de * nv;
+  const int e0 = lane / nv, v0 = lane - e0 * nv;
+  // The ids of all entries first (-1 for an invalid one). Positions come from the
+  // scan; one out of range is reported (the search then fails) instead of being
+  // dereferenced.
+  for (int i = lane; i < cnt; i += 64) {
+    const int32_t pos = a.short_pos[q * a.K + i];
+    const int64_t id = (pos >= 0 && pos < a.positions) ? a.ids[pos] : -1;
+    const bool ok = id >= 0 && id < a.n;
+    if (!ok) atomicAdd(a.invalid, 1ull);
+    rid[i] = ok ? id : -1;
+  }
   __syncthreads();
-  for (int k = 2; k <= M; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = lane; i < M; i += 64) {
-        const int p = i ^ j;
-        if (p > i) {
-          const uint64_t x = keys[i], y = keys[p];
-          if ((x > y) == ((i & k) == 0)) {
-            keys[i] = y;
-            keys[p] = x;
-          }
+  for (int c0 = 0; c0 < cnt; c0 += R) {
+    const int n = cnt - c0 < R ? cnt - c0 : R;
+    const int total = n * nv;
+    int e = e0, v = v0;
+    for (int base = 0; base < total; base += 64 * kStageLoads) {
+      float4 x[kStageLoads];
+      int at[kStageLoads];
+#pragma unroll
+      for (int u = 0; u < kStageLoads; ++u) {
+        const bool in = base + 64 * u + lane < total;
+        const int64_t id = in ? rid[c0 + e] : -1;
+        x[u] = id >= 0 ? *reinterpret_cast<const float4*>(a.dataset + id * a.dim + 4 * v)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        at[u] = in ? e * stride + 4 * v : -1;
+        e += de;
+        v += dv;
+        if (v >= nv) {
+          v -= nv;
+          ++e;
         }
       }
-      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < kStageLoads; ++u)
+        if (at[u] >= 0) *reinterpret_cast<float4*>(rows + at[u]) = x[u];
     }
-  }
-  const int64_t kk = a.k < cnt ? a.k : cnt;
-  for (int64_t t = lane; t < a.k; t += 64) {
-    int64_t id = -1;
-    float d = __builtin_inff();
-    if (t < kk && keys[t] != kNoKey) {
-      const int i = static_cast<int>(keys[t] & 0xffffffffu);
-      id = a.ids[a.short_pos[q * a.K + i]];
-      d = a.metric == kIP ? -vals[i] : vals[i];
+    __syncthreads();
+    if (lane < n) {
+      const int64_t id = rid[c0 + lane];
+      uint64_t key = kNoKey;
+      if (id >= 0) {
+        const float val = metric_value(a.metric, qs, rows + lane * stride, a.dim, a.qnorm[q], a.xnorm[id]);
+        key = make_key(val, static_cast<uint32_t>(c0 + lane));
+        vals[c0 + lane] = val;
+      }
+      keys[c0 + lane] = key;
     }
-    a.out_ids[q * a.k + t] = id;
-    a.out_dist[q * a.k + t] = d;
+    __syncthreads();
   }
+  for (int i = cnt + lane; i < M; i += 64) keys[i] = kNoKey;
+  sort_and_publish(a, q, keys, vals, M, cnt, rid);
 }
 
 // Shortlists of at most 16 (M <= 16): four queries per wave64, 16 lanes each, so a
@@ -267,6 +382,16 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
     if (lds4 <= 65536) {
       const int64_t blocks = (a.nq + kGroups - 1) / kGroups + stat_groups;
       hipLaunchKernelGGL(k_refine4, dim3(static_cast<uint32_t>(blocks)), dim3(64), lds4, stream, a);
+      return hipGetLastError();
+    }
+  }
+  if ((a.dim & 3) == 0 && (a.dim >> 2) <= kStageVecMax) {
+    const int stride = a.dim + 4;
+    const int R = static_cast<int>(std::min<size_t>(kStageRowsMax, kStageBytes / (static_cast<size_t>(stride) * 4)));
+    const StagedCarve c = staged_carve(a.dim, M, R, stride);
+    if (R >= 4 && c.lds <= 65536) {
+      hipLaunchKernelGGL(k_refine_staged, dim3(static_cast<uint32_t>(a.nq + stat_groups)), dim3(64),
+                         c.lds, stream, a, M, R, stride);
       return hipGetLastError();
     }
   }
