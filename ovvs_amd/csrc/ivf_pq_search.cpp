@@ -42,6 +42,12 @@ size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
 // Budget for one chunk of the [queries x nlist] coarse score matrix.
 constexpr size_t kScoreChunkBytes = size_t(512) << 20;
+// Batches of fewer queries than this (the scan's workgroups then number fewer than the
+// compute units) skip the query order, which only decides which queries share an
+// XCD's L2, and take the search counters from the refine launch's last workgroup
+// instead of a copy (every workgroup of that launch takes a ticket from one counter,
+// which costs more than the copy once there are thousands of them).
+constexpr int64_t kSmallBatch = 256;
 
 int64_t elapsed_ns(Clock::time_point a, Clock::time_point b) {
   const auto d = std::chrono::duration_cast<std::chrono::nanoseconds>(b - a).count();
@@ -219,20 +225,29 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // Host outputs: the refine kernel writes straight into the pinned staging buffer
     // (mapped into the device's address space), which replaces two device-to-host
     // copies; they reach the caller's arrays only after the checks below.
+    // Small batches take the search counters the same way (the refine launch's last
+    // workgroup writes them); the scratch entry's counters land in host stack memory
+    // by a copy.
+    const bool small = nq < kSmallBatch;
     bool direct_out = false;
-    if (io == Io::kHost) {
+    unsigned long long* d_cnt_out = nullptr;
+    if (io != Io::kScratch) {
       void* pdev = nullptr;
       if (hipHostGetDevicePointer(&pdev, res->pinned, 0) == hipSuccess && pdev) {
-        d_oid = reinterpret_cast<int64_t*>(static_cast<unsigned char*>(pdev) + pin_ids);
-        d_odist = reinterpret_cast<float*>(static_cast<unsigned char*>(pdev) + pin_dist);
-        direct_out = true;
+        if (small) d_cnt_out = static_cast<unsigned long long*>(pdev);
+        if (io == Io::kHost) {
+          d_oid = reinterpret_cast<int64_t*>(static_cast<unsigned char*>(pdev) + pin_ids);
+          d_odist = reinterpret_cast<float*>(static_cast<unsigned char*>(pdev) + pin_dist);
+          direct_out = true;
+        }
       } else {
         (void)hipGetLastError();
       }
     }
     // counters: [0] candidate rows, [1] non-empty probed lists, [2] shortlist entries,
     // [3] out-of-range probe ids or shortlist positions, [4] queries handed off to the
-    // full-table scan (as unsigned int); [5, 8) unused.
+    // full-table scan (as unsigned int), [5] the refine launch's finished workgroups (as
+    // unsigned int); [6, 8) unused.
     unsigned long long* d_counters = cv.take<unsigned long long>(8);
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
     if (!device_io && bitset) d_bitset = cv.take<uint8_t>(bitset_bytes);
@@ -315,9 +330,11 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       }
     }
     // The scan's query order (counted in the probe-selection stage, so that the scan
-    // stage times the scan kernel alone).
-    SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist, d_okeys,
-                                    mfma_probe ? 1 : 0, d_order, s));
+    // stage times the scan kernel alone); small batches skip it.
+    const bool ordered = !small;
+    if (ordered)
+      SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist,
+                                      d_okeys, mfma_probe ? 1 : 0, d_order, s));
     SEARCH_HIP(hipEventRecord(ev[2], s));
 
     OvvsScanArgs sa{};
@@ -343,7 +360,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     sa.list_grp = dv.list_grp.as<int32_t>();
     sa.grp_seg = dv.grp_seg.as<int32_t>();
     sa.grp_box = dv.box_dims > 0 ? dv.grp_box.as<uint32_t>() : nullptr;
-    sa.order = d_order;
+    sa.order = ordered ? d_order : nullptr;
     sa.positions = dv.positions;
     sa.codes = dv.codes.as<uint8_t>();
     sa.ids = dv.ids.as<int64_t>();
@@ -383,13 +400,18 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.invalid = d_counters + 3;
     ra.stats = d_sstats;  // the scan's per-query statistics, summed by the same launch
     ra.counters = d_counters;
+    ra.counters_out = d_cnt_out;
+    ra.done = reinterpret_cast<unsigned int*>(d_counters + 5);
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
     SEARCH_HIP(hipEventRecord(ev[4], s));
-    work.kernel_launches += (mfma_probe ? 3 + chunks : 5 + 2 * chunks) + (table_ok ? 1 : 0);
+    work.kernel_launches +=
+        (mfma_probe ? 3 + chunks : 5 + 2 * chunks) + (table_ok ? 1 : 0) - (ordered ? 0 : 1);
 
-    SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
-    ovvs::saturating_add(work.d2h_calls, 1);
-    ovvs::saturating_add(work.d2h_bytes, 40);
+    if (!d_cnt_out) {
+      SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
+      ovvs::saturating_add(work.d2h_calls, 1);
+      ovvs::saturating_add(work.d2h_bytes, 40);
+    }
     if (!device_io && !direct_out) {
       SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
       SEARCH_HIP(hipMemcpyAsync(pin + pin_dist, d_odist, nqk * 4, hipMemcpyDeviceToHost, s));

@@ -222,6 +222,11 @@ struct OvvsRefineArgs {
   // workgroups of the same launch.
   const int32_t* stats;
   unsigned long long* counters;
+  // Optional: the launch's last workgroup copies counters[0, 5) here (host memory
+  // mapped into the device's address space) after every other workgroup's atomics;
+  // done is its ticket counter, zero before the launch.
+  unsigned long long* counters_out;
+  unsigned int* done;
 };
 
 // Exact re-rank of each query's shortlist by the index metric and final select

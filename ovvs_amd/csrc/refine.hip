@@ -139,11 +139,28 @@ __device__ void sort_and_publish(const OvvsRefineArgs& a, int64_t q, uint64_t* k
   }
 }
 
-__global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
-  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
-    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
-    return;
+// With counters_out (host memory mapped into the device's address space), the last
+// workgroup of the launch to finish copies the five search counters there once
+// every other workgroup's atomics are done (each fences before taking its ticket),
+// so the host reads them after its stream synchronization without a copy.
+__device__ void publish_counters(const OvvsRefineArgs& a) {
+  if (!a.counters_out) return;
+  __shared__ bool last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    last = atomicAdd(a.done, 1u) == gridDim.x - 1u;
   }
+  __syncthreads();
+  if (last) {
+    __threadfence();
+    if (threadIdx.x < 5)
+      a.counters_out[threadIdx.x] =
+          __hip_atomic_load(a.counters + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ void refine_one(const OvvsRefineArgs& a, int Mmax) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* qs = reinterpret_cast<float*>(smem);
   uint64_t* keys =
@@ -179,6 +196,15 @@ __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax)
   sort_and_publish(a, q, keys, vals, M, cnt, nullptr);
 }
 
+__global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
+  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
+    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
+  } else {
+    refine_one(a, Mmax);
+  }
+  publish_counters(a);
+}
+
 // Shortlists longer than 16 with dim % 4 == 0 (dim <= 4 * kStageVecMax): the rows
 // of R entries at a time are read by the whole wave, consecutive lanes taking
 // consecutive 16-byte vectors of a row (a load instruction covers whole rows instead
@@ -206,12 +232,7 @@ __host__ __device__ inline StagedCarve staged_carve(int dim, int M, int R, int s
   return c;
 }
 
-__global__ __launch_bounds__(64) void k_refine_staged(const OvvsRefineArgs a, int Mmax, int R,
-                                                      int stride) {
-  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
-    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
-    return;
-  }
+__device__ void refine_staged_one(const OvvsRefineArgs& a, int Mmax, int R, int stride) {
   extern __shared__ __align__(16) unsigned char smem[];
   const StagedCarve L = staged_carve(a.dim, Mmax, R, stride);
   float* qs = reinterpret_cast<float*>(smem);
@@ -284,6 +305,16 @@ __global__ __launch_bounds__(64) void k_refine_staged(const OvvsRefineArgs a, in
   sort_and_publish(a, q, keys, vals, M, cnt, rid);
 }
 
+__global__ __launch_bounds__(64) void k_refine_staged(const OvvsRefineArgs a, int Mmax, int R,
+                                                      int stride) {
+  if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
+    refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
+  } else {
+    refine_staged_one(a, Mmax, R, stride);
+  }
+  publish_counters(a);
+}
+
 // Shortlists of at most 16 (M <= 16): four queries per wave64, 16 lanes each, so a
 // batch needs a quarter of the waves. Lane i of a group scores entry i; the 16 keys
 // of each group are sorted by the same bitonic network in LDS.
@@ -295,12 +326,7 @@ size_t refine4_lds(int dim) {
          static_cast<size_t>(64) * 12;
 }
 
-__global__ __launch_bounds__(64) void k_refine4(const OvvsRefineArgs a) {
-  const int64_t nblk = (a.nq + kGroups - 1) / kGroups;
-  if (static_cast<int64_t>(blockIdx.x) >= nblk) {
-    refine_stats(a, blockIdx.x - nblk, gridDim.x - nblk);
-    return;
-  }
+__device__ void refine4_one(const OvvsRefineArgs& a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int dq = (a.dim + 3) & ~3;
   float* qs_all = reinterpret_cast<float*>(smem);
@@ -361,6 +387,16 @@ __global__ __launch_bounds__(64) void k_refine4(const OvvsRefineArgs a) {
   }
 }
 
+__global__ __launch_bounds__(64) void k_refine4(const OvvsRefineArgs a) {
+  const int64_t nblk = (a.nq + kGroups - 1) / kGroups;
+  if (static_cast<int64_t>(blockIdx.x) >= nblk) {
+    refine_stats(a, blockIdx.x - nblk, gridDim.x - nblk);
+  } else {
+    refine4_one(a);
+  }
+  publish_counters(a);
+}
+
 }  // namespace
 
 extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t stream) {
@@ -372,7 +408,8 @@ extern "C" hipError_t ovvs_hip_refine(const OvvsRefineArgs* args, hipStream_t st
       a.dim <= 0 ||
       a.K <= 0 ||
       a.K > OVVS_HIP_MAX_REFINE || a.k <= 0 || a.nq > 0x7fffffff - 64 ||
-      (a.stats == nullptr) != (a.counters == nullptr))
+      (a.stats == nullptr) != (a.counters == nullptr) ||
+      (a.counters_out != nullptr && (a.counters == nullptr || a.done == nullptr)))
     return hipErrorInvalidValue;
   int M = 1;
   while (M < a.K) M <<= 1;
