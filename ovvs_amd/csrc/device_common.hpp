@@ -71,11 +71,11 @@ __device__ __forceinline__ float seq_dot_v4(const float* __restrict__ q,
 }
 
 // seq_dot(q, x, d) for d % 4 == 0 with both rows 16-byte aligned (q typically in LDS,
-// x a row in global memory): the same left-to-right sum from +0, x read twelve 16-byte
+// x a row in global memory): the same left-to-right sum from +0, x read kChunk 16-byte
 // vectors at a time with all of a chunk's loads issued before its terms are added, so
 // that a row costs a few memory round trips instead of one per four vectors.
+template <int kChunk = 12>
 __device__ __forceinline__ float seq_dot_v4_chunked(const float* q, const float* __restrict__ x, int d) {
-  constexpr int kChunk = 12;
   const float4* q4 = reinterpret_cast<const float4*>(q);
   const float4* x4 = reinterpret_cast<const float4*>(x);
   const int n4 = d >> 2;

@@ -222,9 +222,17 @@ __device__ float candidate_bound(float t, float qn, float qcn, float cn_max, flo
 
 // Tiles per batch of operand loads: every batch requests the B fragments of kG
 // tiles (and their centred norms) before its matrix-core products.
-template <int KS>
+// Tiles per operand batch, and 16-byte vectors per round trip of the exact re-score.
+// The wide shapes (LDS for one workgroup per CU, registers for two waves per SIMD)
+// keep about three times the vectors in flight, and with operands in registers twice
+// the tiles (the LDS-operand shapes already request a k-step ahead).
+template <int KS, bool WIDE>
 constexpr int batch_tiles() {
-  return 4;
+  return WIDE && KS > 0 ? 8 : 4;
+}
+template <bool WIDE>
+constexpr int rescore_chunk() {
+  return WIDE ? 32 : 12;
 }
 
 // KS in 1..4: the queries' operand fragments are held in registers (dim <= 128);
@@ -235,13 +243,13 @@ constexpr int batch_tiles() {
 // candidates), a 10k-query batch's 625 workgroups run in one round on 256 CUs instead
 // of 1.2. The LDS-operand shapes keep the compiler's allocation (their LDS allows one
 // workgroup per CU).
-template <int KS, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 ? 6 : 1))) void k_probe_mfma(
+template <int KS, int NW, bool WIDE>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WIDE ? 2 : KS > 0 ? 6 : 1))) void k_probe_mfma(
     const OvvsProbeArgs p, const ProbeShape shape) {
   constexpr int kWaves = NW;
   constexpr int kThreads = 64 * NW;
   constexpr int kRowsPerWave = kRows / kWaves;  // rows each wave selects and ranks
-  constexpr int kG = batch_tiles<KS>();
+  constexpr int kG = batch_tiles<KS, WIDE>();
   extern __shared__ __align__(16) unsigned char smem[];
   const Carve L = carve(smem, shape);
   const int lane = lane_id();
@@ -510,7 +518,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(KS > 0 
     const uint32_t c = static_cast<uint32_t>(*s);
     const float* crow = p.centroids + static_cast<int64_t>(c) * dim;
     const float* qrow = L.qs + row * dq;
-    const float dot = (dim & 3) == 0 ? seq_dot_v4_chunked(qrow, crow, dim) : seq_dot(qrow, crow, dim);
+    const float dot =
+        (dim & 3) == 0 ? seq_dot_v4_chunked<rescore_chunk<WIDE>()>(qrow, crow, dim) : seq_dot(qrow, crow, dim);
     *s = make_key((L.qn[row] + p.cnorm[c]) - 2.f * dot, c);
   }
   wave_sync();
@@ -607,26 +616,29 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
   return sh->lds <= 160 * 1024;
 }
 
-template <int KS, int NW>
+template <int KS, int NW, bool WIDE>
 hipError_t launch_probe_nw(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
   if (sh.lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<KS, NW>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_probe_mfma<KS, NW, WIDE>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(sh.lds));
     if (e != hipSuccess) return e;
   }
   const int64_t blocks = (p.nq + kRows - 1) / kRows;
-  hipLaunchKernelGGL((k_probe_mfma<KS, NW>), dim3(static_cast<uint32_t>(blocks)), dim3(64 * NW),
+  hipLaunchKernelGGL((k_probe_mfma<KS, NW, WIDE>), dim3(static_cast<uint32_t>(blocks)), dim3(64 * NW),
                      sh.lds, stream, p, sh);
   return hipGetLastError();
 }
 
 // 16 waves per workgroup when the batch gives fewer workgroups than the 256 CUs
-// (small batches: the latency of one workgroup is the launch), else 8.
+// (small batches: the latency of one workgroup is the launch), else 8; the wide
+// instance of 8 waves when the LDS of two workgroups does not fit a CU.
 template <int KS>
 hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
-  if ((p.nq + kRows - 1) / kRows < 256) return launch_probe_nw<KS, 16>(p, sh, stream);
-  return launch_probe_nw<KS, 8>(p, sh, stream);
+  if ((p.nq + kRows - 1) / kRows < 256) return launch_probe_nw<KS, 16, false>(p, sh, stream);
+  if (2 * sh.lds > 160 * 1024 && sh.gt >= batch_tiles<KS, true>())
+    return launch_probe_nw<KS, 8, true>(p, sh, stream);
+  return launch_probe_nw<KS, 8, false>(p, sh, stream);
 }
 
 }  // namespace
