@@ -354,9 +354,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WIDE ? 
 
   // A wave takes the chunks wave, wave + kWaves, ..., starting at a rotation that
   // differs between neighbouring workgroups of an XCD (blockIdx.x / 8), so that they
-  // do not all miss in L2 on the same tiles at the same time.
+  // do not all miss in L2 on the same tiles at the same time. Operand copies larger
+  // than 8 MB (1 KB per tile and k-step) do not fit an XCD's L2: there the
+  // workgroups keep one order and share what the L2 holds of their current chunks
+  // (C5's 12 MB probe measured 3% faster so, C2's and C3's 4-5% slower).
   const int nmine = (nch - wave + kWaves - 1) / kWaves;
-  const int rot = nmine > 0 ? static_cast<int>((blockIdx.x >> 3) % static_cast<uint32_t>(nmine)) : 0;
+  const bool rotate = static_cast<int64_t>(shape.ntile) * ks <= 8192;
+  const int rot = rotate && nmine > 0 ? static_cast<int>((blockIdx.x >> 3) % static_cast<uint32_t>(nmine)) : 0;
   auto chunk_of = [&](int i) {
     const int j = i + rot;
     return wave + kWaves * (j >= nmine ? j - nmine : j);
