@@ -220,10 +220,9 @@ __device__ float candidate_bound(float t, float qn, float qcn, float cn_max, flo
   return f;
 }
 
-// Tiles per batch of operand loads: every batch requests the B fragments of kG
-// tiles (and their centred norms) before its matrix-core products.
-// Tiles per operand batch, and 16-byte vectors per round trip of the exact re-score.
-// The wide shapes (LDS for one workgroup per CU, registers for two waves per SIMD)
+// Tiles per operand batch (every batch requests the B fragments of its tiles and
+// their centred norms before its matrix-core products), and 16-byte vectors per round
+// trip of the exact re-score. The wide shapes (LDS for one workgroup per CU, registers for two waves per SIMD)
 // keep about three times the vectors in flight, and with operands in registers twice
 // the tiles (the LDS-operand shapes already request a k-step ahead).
 template <int KS, bool WIDE>
