@@ -186,8 +186,8 @@ hipError_t ovvs_hip_scan_table(const OvvsScanArgs* args, hipStream_t stream);
 // P > 1024).
 size_t ovvs_hip_scan_table_lds_bytes(int32_t pq_m, int32_t ks, int32_t dim, int32_t K, int32_t P);
 // order = the queries 0 .. nq-1 sorted by the spatial rank (list_rank, a permutation
-// of the lists) of their nearest probed list (probes[q * P]); the scan hands each
-// XCD one contiguous part of it, so that its L2 serves lists near each other.
+// of the lists) of their nearest probed list (probes[q * P]); the scan's workgroups
+// take it in turn, so that the queries resident on an XCD probe lists near each other.
 // keys: [nq] workspace; with keys_ready it already holds every query's bucket
 // (list_rank[probes[q * P]] >> ovvs_hip_query_key_shift(nlist)).
 hipError_t ovvs_hip_query_order(const int32_t* probes, int64_t nq, int32_t P, const int32_t* list_rank,
