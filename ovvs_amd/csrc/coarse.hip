@@ -335,7 +335,8 @@ __global__ __launch_bounds__(256) void k_probe_fallback(
     const float* __restrict__ Q, const float* __restrict__ qn, int64_t nq,
     const float* __restrict__ C, const float* __restrict__ cn, int nlist, int dim,
     const int32_t* __restrict__ flags, float* __restrict__ S, int P, int M,
-    int32_t* __restrict__ out) {
+    int32_t* __restrict__ out, unsigned long long* stamp) {
+  if (stamp && blockIdx.x == 0 && threadIdx.x == 0) *stamp = wall_clock64();
   extern __shared__ uint64_t sel[];  // [M]
   __shared__ uint32_t hist[256];
   __shared__ uint32_t scan_scratch[4];
@@ -412,7 +413,8 @@ extern "C" hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t 
 extern "C" hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, int64_t nq,
                                               const float* C, const float* cn, int32_t nlist,
                                               int32_t dim, const int32_t* flags, float* S,
-                                              int32_t P, int32_t* out, hipStream_t stream) {
+                                              int32_t P, int32_t* out, unsigned long long* stamp,
+                                              hipStream_t stream) {
   if (nq <= 0) return hipSuccess;
   if (!Q || !qn || !C || !cn || !flags || !S || !out || nlist <= 0 || dim <= 0 || P <= 0 ||
       P > nlist || P > OVVS_HIP_MAX_PROBES || nq > 0x7fffffff)
@@ -421,6 +423,6 @@ extern "C" hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, i
   while (M < P) M <<= 1;
   hipLaunchKernelGGL(k_probe_fallback, dim3(static_cast<uint32_t>((nq + kFallbackRows - 1) / kFallbackRows)), dim3(256),
                      static_cast<size_t>(M) * sizeof(uint64_t), stream, Q, qn, nq, C, cn, nlist,
-                     dim, flags, S, P, M, out);
+                     dim, flags, S, P, M, out, stamp);
   return hipGetLastError();
 }

@@ -171,6 +171,8 @@ struct ovvsResourcesImpl {
   hipStream_t stream = nullptr;
   static constexpr int kEvents = 6;
   hipEvent_t events[kEvents] = {};
+  // Rate of the device wall clock (wall_clock64) the kernels' stage stamps read, kHz.
+  double wall_khz = 1e5;
   ovvs::DeviceBuffer workspace;
   void* pinned = nullptr;
   size_t pinned_bytes = 0;

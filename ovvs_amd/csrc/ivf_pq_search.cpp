@@ -172,7 +172,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     fixed += align256(static_cast<size_t>(nq) * 16);                    // scan statistics
     fixed += align256(static_cast<size_t>(nq) * 4);                     // full-table handoffs
     fixed += device_io ? 0 : align256(nqk * 8) + align256(nqk * 4);     // staged outputs
-    fixed += align256(8 * 8);                                           // counters
+    fixed += align256(16 * 8);                                          // counters, stamps
     fixed += (!device_io && bitset) ? align256(bitset_bytes) : 0;
     // Query chunk of the coarse score matrix (the exact route and the probe's
     // fallback work through it chunk by chunk).
@@ -199,9 +199,9 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     if (io == Io::kHost) {
       SEARCH_TRY(res->reserve_pinned(pin_bits + (bitset ? bitset_bytes : 0)));
     } else if (io == Io::kDevice) {
-      SEARCH_TRY(res->reserve_pinned(64));
+      SEARCH_TRY(res->reserve_pinned(16 * 8));
     }
-    unsigned long long scratch_counters[5] = {0, 0, 0, 0, 0};
+    unsigned long long scratch_counters[16] = {};
     unsigned char* pin = io == Io::kScratch ? reinterpret_cast<unsigned char*>(scratch_counters)
                                             : static_cast<unsigned char*>(res->pinned);
 
@@ -247,8 +247,12 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // counters: [0] candidate rows, [1] non-empty probed lists, [2] shortlist entries,
     // [3] out-of-range probe ids or shortlist positions, [4] queries handed off to the
     // full-table scan (as unsigned int), [5] the refine launch's finished workgroups (as
-    // unsigned int); [6, 8) unused.
-    unsigned long long* d_counters = cv.take<unsigned long long>(8);
+    // unsigned int); [6, 8) unused; [8, 13) the device wall clock when the probe, its
+    // fallback, the scan and the refine start and when the refine ends (the stage times
+    // of the matrix-core route; its first four are written by those launches, the end by
+    // the refine's last workgroup with the counters of a small batch).
+    unsigned long long* d_counters = cv.take<unsigned long long>(16);
+    unsigned long long* d_stamps = d_counters + 8;
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
     if (!device_io && bitset) d_bitset = cv.take<uint8_t>(bitset_bytes);
     float* d_scores = cv.take<float>(static_cast<size_t>(qc) * ix.nlist);
@@ -279,8 +283,14 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // The matrix-core probe computes the query norms and clears the counters itself.
     if (!mfma_probe) SEARCH_HIP(hipMemsetAsync(d_counters, 0, 8 * 8, s));
 
+    // Stage times: the matrix-core route reads the launches' stamps, and records two
+    // events around the search only when the refine's end is not stamped (each event
+    // recorded between launches adds a few microseconds to the chain); the exact
+    // route records an event at every stage boundary.
     hipEvent_t* ev = res->events;
-    SEARCH_HIP(hipEventRecord(ev[0], s));
+    const bool stamped = mfma_probe;
+    const bool end_stamped = stamped && d_cnt_out != nullptr;
+    if (!end_stamped) SEARCH_HIP(hipEventRecord(ev[0], s));
     if (!mfma_probe) SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
     int64_t chunks = 0;
     if (mfma_probe) {
@@ -306,14 +316,15 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       pa.cnc_max = dv.cnc_max;
       pa.probes = d_probes;
       pa.fallback = d_flags;
+      pa.stamp = d_stamps;
       SEARCH_HIP(ovvs_hip_probe_mfma(&pa, s));
-      SEARCH_HIP(hipEventRecord(ev[1], s));
       for (int64_t q0 = 0; q0 < nq; q0 += qc) {
         const int64_t cnt = std::min(qc, nq - q0);
         SEARCH_HIP(ovvs_hip_probe_fallback(d_q + q0 * dim, d_qn + q0, cnt,
                                            dv.centroids.as<float>(), dv.cnorm.as<float>(),
                                            ix.nlist, dim, d_flags + q0, d_scores, P,
-                                           d_probes + q0 * P, s));
+                                           d_probes + q0 * P, q0 == 0 ? d_stamps + 1 : nullptr,
+                                           s));
         ++chunks;
       }
       work.kernel_launches += 1;
@@ -335,7 +346,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     if (ordered)
       SEARCH_HIP(ovvs_hip_query_order(d_probes, nq, P, dv.list_rank.as<int32_t>(), ix.nlist,
                                       d_okeys, mfma_probe ? 1 : 0, d_order, s));
-    SEARCH_HIP(hipEventRecord(ev[2], s));
+    if (!stamped) SEARCH_HIP(hipEventRecord(ev[2], s));
 
     OvvsScanArgs sa{};
     sa.queries = d_q;
@@ -376,9 +387,10 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
         ovvs_hip_scan_table_lds_bytes(ix.pq_m, ix.pq_ks, dim, R, P) != 0;
     sa.punt = table_ok ? d_punt : nullptr;
     sa.punt_count = reinterpret_cast<unsigned int*>(d_counters + 4);
+    sa.stamp = stamped ? d_stamps + 2 : nullptr;
     SEARCH_HIP(ovvs_hip_scan(&sa, s));
     if (table_ok) SEARCH_HIP(ovvs_hip_scan_table(&sa, s));
-    SEARCH_HIP(hipEventRecord(ev[3], s));
+    if (!stamped) SEARCH_HIP(hipEventRecord(ev[3], s));
 
     OvvsRefineArgs ra{};
     ra.queries = d_q;
@@ -402,15 +414,17 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.counters = d_counters;
     ra.counters_out = d_cnt_out;
     ra.done = reinterpret_cast<unsigned int*>(d_counters + 5);
+    ra.stamps = stamped ? d_stamps : nullptr;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
-    SEARCH_HIP(hipEventRecord(ev[4], s));
+    if (!end_stamped) SEARCH_HIP(hipEventRecord(ev[4], s));
     work.kernel_launches +=
         (mfma_probe ? 3 + chunks : 5 + 2 * chunks) + (table_ok ? 1 : 0) - (ordered ? 0 : 1);
 
     if (!d_cnt_out) {
-      SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
+      const size_t words = stamped ? 12 : 5;  // the counters, and the four start stamps
+      SEARCH_HIP(hipMemcpyAsync(pin, d_counters, words * 8, hipMemcpyDeviceToHost, s));
       ovvs::saturating_add(work.d2h_calls, 1);
-      ovvs::saturating_add(work.d2h_bytes, 40);
+      ovvs::saturating_add(work.d2h_bytes, static_cast<int64_t>(words * 8));
     }
     if (!device_io && !direct_out) {
       SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
@@ -420,7 +434,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     }
     ovvs::saturating_add(work.wait_calls, 1);
     SEARCH_HIP(hipStreamSynchronize(s));
-    unsigned long long counters[5];
+    unsigned long long counters[13];
     std::memcpy(counters, pin, sizeof(counters));
     // A probe id or shortlist position out of range is an internal error: the
     // kernels count it instead of dereferencing it, and nothing is published.
@@ -439,14 +453,34 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     d.tasks = static_cast<int64_t>(std::min<unsigned long long>(counters[1], INT64_MAX));
     d.candidate_rows = static_cast<int64_t>(std::min<unsigned long long>(counters[0], INT64_MAX));
     d.selected_rows = static_cast<int64_t>(std::min<unsigned long long>(counters[2], INT64_MAX));
-    if (chunks == 1) {
+    if (stamped) {
+      // Stamps are wall-clock ticks of the device; a stage is the time from its first
+      // launch's start to the next stage's (the refine: to its end, or the events'
+      // span less the earlier stages).
+      const unsigned long long* t = counters + 8;
+      auto span = [&](unsigned long long a, unsigned long long b) -> int64_t {
+        return b > a ? static_cast<int64_t>(static_cast<double>(b - a) * 1e6 / res->wall_khz) : 0;
+      };
+      d.coarse_pairwise_ns = span(t[0], t[1]);
+      d.coarse_topk_ns = span(t[1], t[2]);
+      d.adc_scan_select_ns = span(t[2], t[3]);
+      if (end_stamped) {
+        d.refine_distance_ns = span(t[3], t[4]);
+      } else {
+        const int64_t before = span(t[0], t[3]);
+        const int64_t all = event_ns(ev[0], ev[4]);
+        d.refine_distance_ns = all > before ? all - before : 0;
+      }
+    } else if (chunks == 1) {
       d.coarse_pairwise_ns = event_ns(ev[0], ev[1]);
       d.coarse_topk_ns = event_ns(ev[1], ev[2]);
+      d.adc_scan_select_ns = event_ns(ev[2], ev[3]);
+      d.refine_distance_ns = event_ns(ev[3], ev[4]);
     } else {
       d.coarse_pairwise_ns = event_ns(ev[0], ev[2]);
+      d.adc_scan_select_ns = event_ns(ev[2], ev[3]);
+      d.refine_distance_ns = event_ns(ev[3], ev[4]);
     }
-    d.adc_scan_select_ns = event_ns(ev[2], ev[3]);
-    d.refine_distance_ns = event_ns(ev[3], ev[4]);
     d.total_wall_ns = elapsed_ns(started, Clock::now());
     int64_t named = 0;
     ovvs::saturating_add(named, d.coarse_pairwise_ns);

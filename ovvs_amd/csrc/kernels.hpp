@@ -91,6 +91,8 @@ struct OvvsProbeArgs {
   float cnc_max;           // max of cnc (+inf if any is NaN or inf)
   int32_t* probes;         // [nq * P] out, rank order (rows with fallback[q] = 0)
   int32_t* fallback;       // [nq] out: 1 where the query needs the exact route
+  unsigned long long* stamp; // or nullptr: the launch's first workgroup writes the
+                             // device wall clock (wall_clock64) at its start here
 };
 
 // 1 when the fused probe handles these shapes.
@@ -111,10 +113,11 @@ hipError_t ovvs_hip_probe_mfma(const OvvsProbeArgs* args, hipStream_t stream);
 // not certify): exact scores of every centroid into S[q*nlist + c] (a scratch of
 // nq * nlist floats), then their first P centroids in rank order into out[q*P ...].
 // Unflagged queries are left untouched.
+// stamp: as OvvsProbeArgs::stamp, or nullptr.
 hipError_t ovvs_hip_probe_fallback(const float* Q, const float* qn, int64_t nq, const float* C,
                                    const float* cn, int32_t nlist, int32_t dim,
                                    const int32_t* flags, float* S, int32_t P, int32_t* out,
-                                   hipStream_t stream);
+                                   unsigned long long* stamp, hipStream_t stream);
 
 // Exact argmin over all centroids for each row of Q (top-1 of the coarse score
 // under the same total order), fused with the score computation: labels[i].
@@ -155,6 +158,7 @@ struct OvvsScanArgs {
   const int64_t* ids;          // [positions] row ids by scan position
   const int32_t* rord;         // [positions] index of each row within its list
   const uint8_t* bitset;       // (n+7)/8 bytes or nullptr
+  unsigned long long* stamp;   // as OvvsProbeArgs::stamp (k_scan's first workgroup), or nullptr
   int32_t K;                   // shortlist length (krefine), 1..OVVS_HIP_MAX_REFINE
   uint64_t* out_keys;          // [nq * K] (score key << 32 | dense ordinal), ascending
   int32_t* out_pos;            // [nq * K] scan positions
@@ -227,6 +231,11 @@ struct OvvsRefineArgs {
   // done is its ticket counter, zero before the launch.
   unsigned long long* counters_out;
   unsigned int* done;
+  // Optional: the search's stage stamps [5] (device wall clock; [0, 3) written by the
+  // probe, fallback and scan launches): the launch's first workgroup writes stamps[3]
+  // when it starts; with counters_out, the last workgroup copies stamps[0, 4) and the
+  // clock at its end to counters_out[8, 13).
+  unsigned long long* stamps;
 };
 
 // Exact re-rank of each query's shortlist by the index metric and final select

@@ -255,6 +255,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WIDE ? 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const int dim = p.dim, dq = shape.dq, ks = shape.ks, nch = shape.nch;
+  if (p.stamp && blockIdx.x == 0 && threadIdx.x == 0) *p.stamp = wall_clock64();
 
   // Stage the 16 query rows (zero past dim and past nq).
   for (int i = static_cast<int>(threadIdx.x); i < kRows * dq; i += kThreads) {

@@ -143,6 +143,8 @@ __device__ void sort_and_publish(const OvvsRefineArgs& a, int64_t q, uint64_t* k
 // workgroup of the launch to finish copies the five search counters there once
 // every other workgroup's atomics are done (each fences before taking its ticket),
 // so the host reads them after its stream synchronization without a copy.
+// With stamps, the last workgroup also copies the stage stamps and its end time to
+// counters_out[8, 13).
 __device__ void publish_counters(const OvvsRefineArgs& a) {
   if (!a.counters_out) return;
   __shared__ bool last;
@@ -157,7 +159,16 @@ __device__ void publish_counters(const OvvsRefineArgs& a) {
     if (threadIdx.x < 5)
       a.counters_out[threadIdx.x] =
           __hip_atomic_load(a.counters + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.stamps && threadIdx.x >= 8 && threadIdx.x < 13)
+      a.counters_out[threadIdx.x] =
+          threadIdx.x == 12 ? wall_clock64()
+                            : __hip_atomic_load(a.stamps + (threadIdx.x - 8), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+__device__ __forceinline__ void stamp_start(const OvvsRefineArgs& a) {
+  if (a.stamps && blockIdx.x == 0 && threadIdx.x == 0) a.stamps[3] = wall_clock64();
 }
 
 __device__ void refine_one(const OvvsRefineArgs& a, int Mmax) {
@@ -197,6 +208,7 @@ __device__ void refine_one(const OvvsRefineArgs& a, int Mmax) {
 }
 
 __global__ __launch_bounds__(64) void k_refine(const OvvsRefineArgs a, int Mmax) {
+  stamp_start(a);
   if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
     refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
   } else {
@@ -307,6 +319,7 @@ __device__ void refine_staged_one(const OvvsRefineArgs& a, int Mmax, int R, int 
 
 __global__ __launch_bounds__(64) void k_refine_staged(const OvvsRefineArgs a, int Mmax, int R,
                                                       int stride) {
+  stamp_start(a);
   if (static_cast<int64_t>(blockIdx.x) >= a.nq) {
     refine_stats(a, blockIdx.x - a.nq, gridDim.x - a.nq);
   } else {
@@ -388,6 +401,7 @@ __device__ void refine4_one(const OvvsRefineArgs& a) {
 }
 
 __global__ __launch_bounds__(64) void k_refine4(const OvvsRefineArgs a) {
+  stamp_start(a);
   const int64_t nblk = (a.nq + kGroups - 1) / kGroups;
   if (static_cast<int64_t>(blockIdx.x) >= nblk) {
     refine_stats(a, blockIdx.x - nblk, gridDim.x - nblk);

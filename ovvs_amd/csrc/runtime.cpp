@@ -226,6 +226,12 @@ ovvsStatus ovvsResourcesImpl::ensure_gpu() {
       return OVVS_STATUS_DEVICE_UNAVAILABLE;
     }
   }
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0) {
+    wall_khz = khz;
+  } else {
+    (void)hipGetLastError();
+  }
   device = dev;
   stream = s;
   for (int i = 0; i < kEvents; ++i) events[i] = ev[i];

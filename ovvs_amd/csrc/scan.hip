@@ -1265,12 +1265,14 @@ template <int KPL, int FD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KPL == 1 ? 6 : 7))) void k_scan(
     const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  if (a.stamp && blockIdx.x == 0 && threadIdx.x == 0) *a.stamp = wall_clock64();
   scan_query<KPL, FD>(a, smem);
 }
 
 template <int KPL>
 __global__ __launch_bounds__(kThreads) void k_scan_long(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  if (a.stamp && blockIdx.x == 0 && threadIdx.x == 0) *a.stamp = wall_clock64();
   scan_query<KPL, 0>(a, smem);
 }
 

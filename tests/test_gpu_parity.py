@@ -422,6 +422,33 @@ def test_telemetry_counts_and_failure_atomicity(ovvs, res, ref_cases, tmp_path):
     ix.close()
 
 
+def test_stage_times_for_small_and_large_batches(ovvs, tmp_path):
+    """Stage times come from the launches' device-clock stamps: batches under 256
+    queries take the refine's end from its last workgroup (no events), larger ones
+    from an event pair around the search. Either way every stage is counted and the
+    stages fit inside the call's host wall time; results do not depend on the path."""
+    rng = np.random.default_rng(5)
+    dim, n = 32, 20000
+    centers = rng.standard_normal((64, dim)).astype(np.float32)
+    data = (centers[rng.integers(0, 64, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
+    q = (centers[rng.integers(0, 64, 600)] + 0.3 * rng.standard_normal((600, dim))).astype(np.float32)
+    r = ovvs.Resources()
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=128, pq_m=16, pq_nbits=8, resources=r)
+    stages = ["coarse_pairwise_ns", "coarse_topk_ns", "adc_scan_select_ns", "refine_distance_ns"]
+    whole_ids, whole_d = ix.search(q, 10, 16, 32)
+    for nq in (1, 100, 255, 256, 600):
+        say("stage times", nq)
+        before = r.ivfpq_search_stats()
+        ids, d = ix.search(q[:nq], 10, 16, 32)
+        after = r.ivfpq_search_stats()
+        delta = {k: after[k] - before[k] for k in stages + ["total_wall_ns"]}
+        for k in stages:
+            assert delta[k] > 0, (nq, k, delta)
+        assert sum(delta[k] for k in stages) <= delta["total_wall_ns"], (nq, delta)
+        assert np.array_equal(ids, whole_ids[:nq]) and np.array_equal(_bits(d), _bits(whole_d[:nq]))
+    ix.close()
+
+
 @pytest.mark.skipif(not REF_SO.exists(), reason="oracle/_ref not built")
 def test_c1_scale_against_reference(ovvs, res, tmp_path):
     """Config 1 (100k x 128, 256 lists, pq 32, 16 probes, k 10, fp32 tables): the
