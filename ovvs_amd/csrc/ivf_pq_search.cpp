@@ -249,8 +249,8 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // full-table scan (as unsigned int), [5] the refine launch's finished workgroups (as
     // unsigned int); [6, 8) unused; [8, 13) the device wall clock when the probe, its
     // fallback, the scan and the refine start and when the refine ends (the stage times
-    // of the matrix-core route; its first four are written by those launches, the end by
-    // the refine's last workgroup with the counters of a small batch).
+    // of small batches on the matrix-core route; the first four are written by those
+    // launches, the end by the refine's last workgroup with the counters).
     unsigned long long* d_counters = cv.take<unsigned long long>(16);
     unsigned long long* d_stamps = d_counters + 8;
     const uint8_t* d_bitset = device_io ? bitset : nullptr;
@@ -283,14 +283,13 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     // The matrix-core probe computes the query norms and clears the counters itself.
     if (!mfma_probe) SEARCH_HIP(hipMemsetAsync(d_counters, 0, 8 * 8, s));
 
-    // Stage times: the matrix-core route reads the launches' stamps, and records two
-    // events around the search only when the refine's end is not stamped (each event
-    // recorded between launches adds a few microseconds to the chain); the exact
-    // route records an event at every stage boundary.
+    // Stage times: small batches on the matrix-core route read the launches' stamps
+    // (each event recorded between launches adds a few microseconds to a chain that
+    // then lasts about 85 us); other searches record a HIP event at every stage
+    // boundary on the search's stream.
     hipEvent_t* ev = res->events;
-    const bool stamped = mfma_probe;
-    const bool end_stamped = stamped && d_cnt_out != nullptr;
-    if (!end_stamped) SEARCH_HIP(hipEventRecord(ev[0], s));
+    const bool stamped = mfma_probe && d_cnt_out != nullptr;
+    if (!stamped) SEARCH_HIP(hipEventRecord(ev[0], s));
     if (!mfma_probe) SEARCH_HIP(ovvs_hip_row_norms(d_q, nq, dim, d_qn, s));
     int64_t chunks = 0;
     if (mfma_probe) {
@@ -316,15 +315,16 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       pa.cnc_max = dv.cnc_max;
       pa.probes = d_probes;
       pa.fallback = d_flags;
-      pa.stamp = d_stamps;
+      pa.stamp = stamped ? d_stamps : nullptr;
       SEARCH_HIP(ovvs_hip_probe_mfma(&pa, s));
+      if (!stamped) SEARCH_HIP(hipEventRecord(ev[1], s));
       for (int64_t q0 = 0; q0 < nq; q0 += qc) {
         const int64_t cnt = std::min(qc, nq - q0);
         SEARCH_HIP(ovvs_hip_probe_fallback(d_q + q0 * dim, d_qn + q0, cnt,
                                            dv.centroids.as<float>(), dv.cnorm.as<float>(),
                                            ix.nlist, dim, d_flags + q0, d_scores, P,
-                                           d_probes + q0 * P, q0 == 0 ? d_stamps + 1 : nullptr,
-                                           s));
+                                           d_probes + q0 * P,
+                                           stamped && q0 == 0 ? d_stamps + 1 : nullptr, s));
         ++chunks;
       }
       work.kernel_launches += 1;
@@ -416,15 +416,14 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     ra.done = reinterpret_cast<unsigned int*>(d_counters + 5);
     ra.stamps = stamped ? d_stamps : nullptr;
     SEARCH_HIP(ovvs_hip_refine(&ra, s));
-    if (!end_stamped) SEARCH_HIP(hipEventRecord(ev[4], s));
+    if (!stamped) SEARCH_HIP(hipEventRecord(ev[4], s));
     work.kernel_launches +=
         (mfma_probe ? 3 + chunks : 5 + 2 * chunks) + (table_ok ? 1 : 0) - (ordered ? 0 : 1);
 
     if (!d_cnt_out) {
-      const size_t words = stamped ? 12 : 5;  // the counters, and the four start stamps
-      SEARCH_HIP(hipMemcpyAsync(pin, d_counters, words * 8, hipMemcpyDeviceToHost, s));
+      SEARCH_HIP(hipMemcpyAsync(pin, d_counters, 5 * 8, hipMemcpyDeviceToHost, s));
       ovvs::saturating_add(work.d2h_calls, 1);
-      ovvs::saturating_add(work.d2h_bytes, static_cast<int64_t>(words * 8));
+      ovvs::saturating_add(work.d2h_bytes, 40);
     }
     if (!device_io && !direct_out) {
       SEARCH_HIP(hipMemcpyAsync(pin + pin_ids, d_oid, nqk * 8, hipMemcpyDeviceToHost, s));
@@ -455,8 +454,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
     d.selected_rows = static_cast<int64_t>(std::min<unsigned long long>(counters[2], INT64_MAX));
     if (stamped) {
       // Stamps are wall-clock ticks of the device; a stage is the time from its first
-      // launch's start to the next stage's (the refine: to its end, or the events'
-      // span less the earlier stages).
+      // launch's start to the next stage's (the refine: to its last workgroup's end).
       const unsigned long long* t = counters + 8;
       auto span = [&](unsigned long long a, unsigned long long b) -> int64_t {
         return b > a ? static_cast<int64_t>(static_cast<double>(b - a) * 1e6 / res->wall_khz) : 0;
@@ -464,13 +462,7 @@ ovvsStatus search_impl(ovvsResources_t res, ovvsIvfPqIndex_t index, const float*
       d.coarse_pairwise_ns = span(t[0], t[1]);
       d.coarse_topk_ns = span(t[1], t[2]);
       d.adc_scan_select_ns = span(t[2], t[3]);
-      if (end_stamped) {
-        d.refine_distance_ns = span(t[3], t[4]);
-      } else {
-        const int64_t before = span(t[0], t[3]);
-        const int64_t all = event_ns(ev[0], ev[4]);
-        d.refine_distance_ns = all > before ? all - before : 0;
-      }
+      d.refine_distance_ns = span(t[3], t[4]);
     } else if (chunks == 1) {
       d.coarse_pairwise_ns = event_ns(ev[0], ev[1]);
       d.coarse_topk_ns = event_ns(ev[1], ev[2]);
