@@ -425,7 +425,16 @@ constexpr int kSegSlots = OVVS_GROUP_SEGMENTS * kSegPerPass;
 constexpr int kItemCap = 256;
 // Phase 0: candidate groups per rank (of the first kWaves ranks) and rounds.
 constexpr int kP0Cand = 64;
+// Shortlists of more than 64 keys (K up to 128) take up to kP0RoundsLong rounds: the
+// union's K-th key needs more rows (C3, k 100: scan 1.25 -> 0.95 ms with 8 rounds instead
+// of 4, while C2 and C4 measured 3% slower with 8).
 constexpr int kP0Rounds = 4;
+constexpr int kP0RoundsLong = 8;
+// misc words after the phase-0 groups misc[4, 4 + kP0RoundsLong): tiles scored after
+// phase 0, rows of the lists whose bound passed.
+constexpr int kMiscTiles = 4 + kP0RoundsLong;
+constexpr int kMiscRows = 5 + kP0RoundsLong;
+static_assert(kMiscRows < 16, "the misc words hold 16 int32");
 // Tiles a query may score after phase 0 before it is handed off to the full-table scan
 // (at least; more when its live lists are large).
 constexpr int kPuntTiles = 32;
@@ -447,7 +456,7 @@ struct ScanLayout {
   size_t resid_off;  // per wave: residual of its current list [dim_pad]
   size_t thr_off;    // [kWaves + 1] published K-th keys (the last: the union's, after phase 0)
   size_t misc_off;   // [16] int32: end of phase 0, bad probe flag, rows, lists, groups
-                     //      scored in phase 0 (kP0Rounds), tiles scored after phase 0,
+                     //      scored in phase 0 (up to kP0RoundsLong), tiles scored after phase 0,
                      //      rows of the lists whose bound passed after phase 0
   size_t slot_off;   // per wave: [2][kSegSlots] int32, the segments of a bound pass and
                      //           their list ranks; before: phase 0's candidate groups
@@ -864,14 +873,15 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       }
     }
   }
-  if (threadIdx.x < kP0Rounds) misc[4 + threadIdx.x] = -1;
-  if (threadIdx.x == kP0Rounds) misc[8] = 0;      // tiles scored after phase 0
-  if (threadIdx.x == kP0Rounds + 1) misc[9] = 0;  // rows of the lists whose bound passed
+  constexpr int kRounds = KPL >= 2 ? kP0RoundsLong : kP0Rounds;
+  if (threadIdx.x < kRounds) misc[4 + threadIdx.x] = -1;
+  if (threadIdx.x == kRounds) misc[kMiscTiles] = 0;  // tiles scored after phase 0
+  if (threadIdx.x == kRounds + 1) misc[kMiscRows] = 0;  // rows of the lists whose bound passed
   __syncthreads();
   // Rounds: the candidate with the smallest bound (ties: the first) is scored; a
   // further round runs while the best remaining candidate's bound does not exceed
   // the union's K-th best score (a group the rest of the search would score anyway).
-  for (int round = 0; round < kP0Rounds; ++round) {
+  for (int round = 0; round < kRounds; ++round) {
     uint64_t best = kNoKey;
     for (int k = lane; k < kWaves * kP0Cand; k += 64) best = p0c[k] < best ? p0c[k] : best;
 #pragma unroll
@@ -1007,9 +1017,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // whose bound does not exceed the K-th best are evaluated the same way, 16 at a
   // time, and the segments kept are scored grouped by list, best bound first within
   // a list.
-  int32_t p0done[kP0Rounds];  // groups phase 0 scored (-1: none)
+  int32_t p0done[kRounds];  // groups phase 0 scored (-1: none), in scalar registers
 #pragma unroll
-  for (int r = 0; r < kP0Rounds; ++r) p0done[r] = misc[4 + r];
+  for (int r = 0; r < kRounds; ++r) p0done[r] = __builtin_amdgcn_readfirstlane(misc[4 + r]);
   int32_t* sslot = reinterpret_cast<int32_t*>(smem + L.slot_off) + wave * 2 * kSegSlots;
   int32_t* sslot_p = sslot + kSegSlots;
   int32_t* it_grp = reinterpret_cast<int32_t*>(smem + L.item_off);
@@ -1025,7 +1035,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     int32_t live = n > 0 ? t_rows[t] : 0;  // rows of the lists whose bound passed
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) live += static_cast<int32_t>(xor_lane(static_cast<uint32_t>(live), o));
-    if (lane == 0) atomicAdd(&misc[9], live);
+    if (lane == 0) atomicAdd(&misc[kMiscRows], live);
     const int32_t incl = wave_incl_scan(n);
     if (t < a.P) {
       t_item[t] = incl - n;  // within the chunk
@@ -1044,9 +1054,9 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
   // more than `budget` tiles (kPuntTiles, or an eighth of the tiles of the lists
   // whose bound passed if that is more), the waves stop scoring, and the query is
   // handed off at the end (its outputs are then written by the full-table scan).
-  const int32_t budget = a.punt ? max(kPuntTiles, misc[9] / (8 * kTile)) : 0x7fffffff;
+  const int32_t budget = a.punt ? max(kPuntTiles, misc[kMiscRows] / (8 * kTile)) : 0x7fffffff;
   auto over_budget = [&]() {
-    return __hip_atomic_load(&misc[8], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > budget;
+    return __hip_atomic_load(&misc[kMiscTiles], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > budget;
   };
   int cur_p = -1;  // list whose residual is in resid
   for (int ib = 0; ib < n_items; ib += kItemCap) {
@@ -1081,7 +1091,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
       refresh();
       bool done = false;
 #pragma unroll
-      for (int r = 0; r < kP0Rounds; ++r) done |= grp == p0done[r];
+      for (int r = 0; r < kRounds; ++r) done |= grp == p0done[r];
       const bool lead = valid && (lane & ((1 << gl) - 1)) == 0 && !done && !(etot > thr_hi);
       for (uint64_t m = __builtin_amdgcn_ballot_w64(lead); m; m &= m - 1) {
         const int b = __builtin_ctzll(m);
@@ -1147,7 +1157,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
         }
         const int32_t st = a.seg_start[gs];
         const int32_t len = a.seg_len[gs];
-        if (lane == 0) atomicAdd(&misc[8], (len + kTile - 1) / kTile);
+        if (lane == 0) atomicAdd(&misc[kMiscTiles], (len + kTile - 1) / kTile);
         for (int32_t t0 = 0; t0 < len; t0 += kTile) {
           const int32_t pos0 = st + t0;
           const int32_t pos = pos0 + lane;
@@ -1242,7 +1252,7 @@ __device__ __forceinline__ void scan_query(const OvvsScanArgs& a, unsigned char*
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) valid += static_cast<int>(xor_lane(static_cast<uint32_t>(valid), o));
-    if (lane == 0 && misc[8] > budget) a.punt[atomicAdd(a.punt_count, 1u)] = static_cast<int32_t>(q);
+    if (lane == 0 && misc[kMiscTiles] > budget) a.punt[atomicAdd(a.punt_count, 1u)] = static_cast<int32_t>(q);
     if (lane == 0) {
       a.out_count[q] = valid;
       // Per-query statistics, summed by the statistics workgroups of the refine
