@@ -62,7 +62,8 @@ hipError_t ovvs_hip_select_topk(const float* S, int64_t ldS, int64_t nrows, int3
 // Limits of the fused probe: dim <= 32 * OVVS_PROBE_MAX_KSTEPS, P <= OVVS_PROBE_MAX_P, at
 // least 2P of its (at most OVVS_PROBE_MAX_GROUPS) centroid groups, its LDS within 160 KiB,
 // at most 256 (P <= 64), 512 (P <= 128) or OVVS_PROBE_CAP (512 where that does not fit
-// the LDS) exact re-scores per query (a query with more takes the exact route).
+// the LDS; 2P + 32, at least 256, where that lets three workgroups share a CU) exact
+// re-scores per query (a query with more takes the exact route).
 #define OVVS_PROBE_MAX_KSTEPS 32
 #define OVVS_PROBE_MAX_P 256
 #define OVVS_PROBE_MAX_GROUPS 512

@@ -42,6 +42,7 @@
 // A query with more candidates than the re-score capacity, or fewer than P (only NaN
 // or infinite inputs can cause that), is flagged in `fallback`; k_probe_fallback
 // (coarse.hip) then ranks it from exact scores of every centroid.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -616,6 +617,20 @@ bool probe_shape(int32_t dim, int32_t nlist, int32_t P, ProbeShape* sh) {
     sh->lds = sh->area_off + (gmin > slot ? gmin : slot);
     if (sh->lds <= 160 * 1024 || sh->cap <= 512) break;
     sh->cap = 512;
+  }
+  // 2P + 32 slots (at least 256) when that lets three workgroups share a CU and the
+  // capacity above does not: a 10k batch's 625 workgroups then run in one round on
+  // 256 CUs instead of two (C3, P 128: 218 candidates per query at the median, 272 at
+  // most; the probe took 0.73 ms with 512 slots). A query with more candidates takes
+  // the exact fallback.
+  {
+    const int cap3 = std::max(256, (2 * P + 32 + 31) & ~31);
+    const size_t slot3 = static_cast<size_t>(kRows) * cap3 * 8;
+    const size_t lds3 = sh->area_off + (gmin > slot3 ? gmin : slot3);
+    if (cap3 < sh->cap && 3 * sh->lds > 160 * 1024 && 3 * lds3 <= 160 * 1024) {
+      sh->cap = cap3;
+      sh->lds = lds3;
+    }
   }
   return sh->lds <= 160 * 1024;
 }
