@@ -1895,9 +1895,15 @@ __host__ __device__ inline bool wave_scan_ok(int pq_m, int ks, int dsub, int dim
          wave_scan_layout(pq_m, ks, dsub, dim).total <= 160u * 1024u;
 }
 
+// part / nparts: the wave scores the lists of probe ranks p with p % nparts == part
+// (every wave still walks all of them for the ordinal bases and statistics). With
+// nparts > 1 every wave of the workgroup takes a part of the same query and
+// `areas` / `area_stride` locate the waves' areas: each publishes its shortlist in
+// its buffers and wave 0 merges them and writes the query's outputs.
 template <int KPL, int DS>
 __device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, const float* cb,
-                                           unsigned char* area, size_t dim_bytes) {
+                                           unsigned char* area, size_t dim_bytes, int part,
+                                           int nparts, unsigned char* areas, size_t area_stride) {
   const int lane = lane_id();
   float* qs = reinterpret_cast<float*>(area);
   float* resid = reinterpret_cast<float*>(area + dim_bytes);
@@ -1964,6 +1970,7 @@ __device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, con
     ++lists;
     ord_base = ord;
     ord += static_cast<uint32_t>(rows);
+    if (p % nparts != part) continue;
     const float* __restrict__ cv = a.centroids + static_cast<int64_t>(l) * dim;
     for (int t = lane; t < dim; t += 64) resid[t] = qs[t] - cv[t];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -2023,6 +2030,34 @@ __device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, con
   } else {
     while (cnt > 0) flush();
   }
+  if (nparts > 1) {
+    // Each wave's list (ascending) in its buffers; wave 0 takes, for every other wave,
+    // the smaller of each of its keys and the other list's mirror (the lower half of a
+    // bitonic merge) and sorts the result: the K smallest keys of the union.
+    static_assert(64 * KPL <= kBufCap, "a wave's list must fit its buffers");
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      bufk[j * 64 + lane] = lk[j];
+      bufp[j * 64 + lane] = lp[j];
+    }
+    __syncthreads();
+    if (part != 0) return;
+    for (int w = 1; w < nparts; ++w) {
+      const unsigned char* wa = areas + static_cast<size_t>(w) * area_stride;
+      const uint64_t* wk = reinterpret_cast<const uint64_t*>(wa + 2 * dim_bytes);
+      const int32_t* wp = reinterpret_cast<const int32_t*>(wa + 2 * dim_bytes + static_cast<size_t>(kBufCap) * 8);
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int e = (KPL - 1 - j) * 64 + (63 - lane);
+        const uint64_t rk = wk[e];
+        if (rk < lk[j]) {
+          lk[j] = rk;
+          lp[j] = wp[e];
+        }
+      }
+      bitonic_merge_asc<KPL>(lk, lp);
+    }
+  }
   int valid = 0;
 #pragma unroll
   for (int j = 0; j < KPL; ++j) {
@@ -2048,7 +2083,9 @@ template <int KPL, int DS>
 __global__ __launch_bounds__(kWaveScanThreads) void k_scan_wave(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const unsigned int n = *a.punt_count;
-  if (blockIdx.x * kWaveScanWaves >= n) return;  // no query for any wave here
+  // No query for this workgroup (one query per workgroup when there are at most as
+  // many as workgroups, else one per wave).
+  if (n <= gridDim.x ? blockIdx.x >= n : blockIdx.x * kWaveScanWaves >= n) return;
   const WaveScanLayout L = wave_scan_layout(a.pq_m, a.ks, DS, a.dim);
   float* cb = reinterpret_cast<float*>(smem + L.cb_off);
   const int n4 = a.pq_m * a.ks * DS / 4;  // ks >= 16: a whole number of 16-byte vectors
@@ -2058,8 +2095,14 @@ __global__ __launch_bounds__(kWaveScanThreads) void k_scan_wave(const OvvsScanAr
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   unsigned char* area = smem + L.wave_off + static_cast<size_t>(wave) * L.wave_stride;
+  if (n <= gridDim.x) {
+    // Few handed-off queries: one per workgroup, its lists dealt to the waves.
+    wave_query<KPL, DS>(a, a.punt[blockIdx.x], cb, area, L.dim_bytes, wave, kWaveScanWaves,
+                        smem + L.wave_off, L.wave_stride);
+    return;
+  }
   for (unsigned int i = blockIdx.x * kWaveScanWaves + wave; i < n; i += gridDim.x * kWaveScanWaves)
-    wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes);
+    wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes, 0, 1, nullptr, 0);
 }
 
 template <int KPL, int DS>
