@@ -1897,9 +1897,11 @@ __host__ __device__ inline bool wave_scan_ok(int pq_m, int ks, int dsub, int dim
 
 // part / nparts: the wave scores the lists of probe ranks p with p % nparts == part
 // (every wave still walks all of them for the ordinal bases and statistics). With
-// nparts > 1 every wave of the workgroup takes a part of the same query and
-// `areas` / `area_stride` locate the waves' areas: each publishes its shortlist in
-// its buffers and wave 0 merges them and writes the query's outputs.
+// nparts > 1, nparts consecutive waves of the workgroup take parts of the same query
+// and `areas` / `area_stride` locate their areas: each publishes its shortlist in its
+// buffers, the part-0 wave merges them and writes the query's outputs. Every wave of
+// the workgroup then passes two barriers (lists published, merge done); k_scan_wave
+// has the waves without a query in that round pass two barriers of their own.
 template <int KPL, int DS>
 __device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, const float* cb,
                                            unsigned char* area, size_t dim_bytes, int part,
@@ -2041,22 +2043,26 @@ __device__ __forceinline__ void wave_query(const OvvsScanArgs& a, int64_t q, con
       bufp[j * 64 + lane] = lp[j];
     }
     __syncthreads();
-    if (part != 0) return;
-    for (int w = 1; w < nparts; ++w) {
-      const unsigned char* wa = areas + static_cast<size_t>(w) * area_stride;
-      const uint64_t* wk = reinterpret_cast<const uint64_t*>(wa + 2 * dim_bytes);
-      const int32_t* wp = reinterpret_cast<const int32_t*>(wa + 2 * dim_bytes + static_cast<size_t>(kBufCap) * 8);
+    if (part == 0) {
+      for (int w = 1; w < nparts; ++w) {
+        const unsigned char* wa = areas + static_cast<size_t>(w) * area_stride;
+        const uint64_t* wk = reinterpret_cast<const uint64_t*>(wa + 2 * dim_bytes);
+        const int32_t* wp =
+            reinterpret_cast<const int32_t*>(wa + 2 * dim_bytes + static_cast<size_t>(kBufCap) * 8);
 #pragma unroll
-      for (int j = 0; j < KPL; ++j) {
-        const int e = (KPL - 1 - j) * 64 + (63 - lane);
-        const uint64_t rk = wk[e];
-        if (rk < lk[j]) {
-          lk[j] = rk;
-          lp[j] = wp[e];
+        for (int j = 0; j < KPL; ++j) {
+          const int e = (KPL - 1 - j) * 64 + (63 - lane);
+          const uint64_t rk = wk[e];
+          if (rk < lk[j]) {
+            lk[j] = rk;
+            lp[j] = wp[e];
+          }
         }
+        bitonic_merge_asc<KPL>(lk, lp);
       }
-      bitonic_merge_asc<KPL>(lk, lp);
     }
+    __syncthreads();  // the other parts' buffers are read
+    if (part != 0) return;
   }
   int valid = 0;
 #pragma unroll
@@ -2083,9 +2089,12 @@ template <int KPL, int DS>
 __global__ __launch_bounds__(kWaveScanThreads) void k_scan_wave(const OvvsScanArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const unsigned int n = *a.punt_count;
-  // No query for this workgroup (one query per workgroup when there are at most as
-  // many as workgroups, else one per wave).
-  if (n <= gridDim.x ? blockIdx.x >= n : blockIdx.x * kWaveScanWaves >= n) return;
+  // G queries per workgroup and round (the smallest power of two covering its share, at
+  // most one per wave), each taken by kWaveScanWaves / G waves.
+  const unsigned int share = (n + gridDim.x - 1) / gridDim.x;
+  unsigned int G = 1;
+  while (G < share && G < static_cast<unsigned int>(kWaveScanWaves)) G <<= 1;
+  if (blockIdx.x * G >= n) return;  // no query for this workgroup in any round
   const WaveScanLayout L = wave_scan_layout(a.pq_m, a.ks, DS, a.dim);
   float* cb = reinterpret_cast<float*>(smem + L.cb_off);
   const int n4 = a.pq_m * a.ks * DS / 4;  // ks >= 16: a whole number of 16-byte vectors
@@ -2095,14 +2104,25 @@ __global__ __launch_bounds__(kWaveScanThreads) void k_scan_wave(const OvvsScanAr
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   unsigned char* area = smem + L.wave_off + static_cast<size_t>(wave) * L.wave_stride;
-  if (n <= gridDim.x) {
-    // Few handed-off queries: one per workgroup, its lists dealt to the waves.
-    wave_query<KPL, DS>(a, a.punt[blockIdx.x], cb, area, L.dim_bytes, wave, kWaveScanWaves,
-                        smem + L.wave_off, L.wave_stride);
+  const int nparts = kWaveScanWaves / static_cast<int>(G);
+  if (nparts == 1) {
+    for (unsigned int i = blockIdx.x * kWaveScanWaves + wave; i < n; i += gridDim.x * kWaveScanWaves)
+      wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes, 0, 1, nullptr, 0);
     return;
   }
-  for (unsigned int i = blockIdx.x * kWaveScanWaves + wave; i < n; i += gridDim.x * kWaveScanWaves)
-    wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes, 0, 1, nullptr, 0);
+  const int g = wave / nparts, part = wave - g * nparts;
+  unsigned char* group_areas = smem + L.wave_off + static_cast<size_t>(g * nparts) * L.wave_stride;
+  const unsigned int rounds = (n + gridDim.x * G - 1) / (gridDim.x * G);
+  for (unsigned int r = 0; r < rounds; ++r) {
+    const unsigned int i = (r * gridDim.x + blockIdx.x) * G + static_cast<unsigned int>(g);
+    if (i < n) {
+      wave_query<KPL, DS>(a, a.punt[i], cb, area, L.dim_bytes, part, nparts, group_areas,
+                          L.wave_stride);
+    } else {
+      __syncthreads();  // as a query's part does: lists published,
+      __syncthreads();  // then merged
+    }
+  }
 }
 
 template <int KPL, int DS>
