@@ -223,16 +223,17 @@ __device__ float candidate_bound(float t, float qn, float qcn, float cn_max, flo
 
 // Tiles per operand batch (every batch requests the B fragments of its tiles and
 // their centred norms before its matrix-core products), and 16-byte vectors per round
-// trip of the exact re-score. The wide shapes (LDS for one workgroup per CU, registers for two waves per SIMD)
-// keep about three times the vectors in flight, and with operands in registers twice
-// the tiles (the LDS-operand shapes already request a k-step ahead).
+// trip of the exact re-score. The wide instance (shapes whose LDS admits one
+// workgroup per CU: sixteen waves, four per SIMD, up to 128 registers each) keeps
+// twice the vectors in flight, and with operands in registers twice the tiles (the
+// LDS-operand shapes already request a k-step ahead).
 template <int KS, bool WIDE>
 constexpr int batch_tiles() {
   return WIDE && KS > 0 ? 8 : 4;
 }
 template <bool WIDE>
 constexpr int rescore_chunk() {
-  return WIDE ? 32 : 12;
+  return WIDE ? 24 : 12;
 }
 
 // KS in 1..4: the queries' operand fragments are held in registers (dim <= 128);
@@ -242,9 +243,9 @@ constexpr int rescore_chunk() {
 // workgroups of eight waves per CU (their LDS allows it up to dim 128 and 256
 // candidates), a 10k-query batch's 625 workgroups run in one round on 256 CUs instead
 // of 1.2. The LDS-operand shapes keep the compiler's allocation (their LDS allows one
-// workgroup per CU).
+// workgroup per CU); the wide instance (sixteen waves) allows four waves per SIMD.
 template <int KS, int NW, bool WIDE>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WIDE ? 2 : KS > 0 ? 6 : 1))) void k_probe_mfma(
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WIDE ? 4 : KS > 0 ? 6 : 1))) void k_probe_mfma(
     const OvvsProbeArgs p, const ProbeShape shape) {
   constexpr int kWaves = NW;
   constexpr int kThreads = 64 * NW;
@@ -650,13 +651,17 @@ hipError_t launch_probe_nw(const OvvsProbeArgs& p, const ProbeShape& sh, hipStre
 }
 
 // 16 waves per workgroup when the batch gives fewer workgroups than the 256 CUs
-// (small batches: the latency of one workgroup is the launch), else 8; the wide
-// instance of 8 waves when the LDS of two workgroups does not fit a CU.
+// (small batches: the latency of one workgroup is the launch) or when the LDS of two
+// workgroups does not fit a CU (the wide instance where its batches fit the chunks:
+// C5's probe took 2.04 ms with eight waves of up to 256 registers, 1.54 with sixteen
+// of 80 and 1.35 with sixteen of 128; C4's 0.61, 0.59 and 0.58), else 8.
 template <int KS>
 hipError_t launch_probe(const OvvsProbeArgs& p, const ProbeShape& sh, hipStream_t stream) {
   if ((p.nq + kRows - 1) / kRows < 256) return launch_probe_nw<KS, 16, false>(p, sh, stream);
-  if (2 * sh.lds > 160 * 1024 && sh.gt >= batch_tiles<KS, true>())
-    return launch_probe_nw<KS, 8, true>(p, sh, stream);
+  if (2 * sh.lds > 160 * 1024) {
+    if (sh.gt >= batch_tiles<KS, true>()) return launch_probe_nw<KS, 16, true>(p, sh, stream);
+    return launch_probe_nw<KS, 16, false>(p, sh, stream);
+  }
   return launch_probe_nw<KS, 8, false>(p, sh, stream);
 }
 

@@ -78,6 +78,27 @@ def test_matrix_core_probe_matches_oracle(ovvs, res, tmp_path, dim, pq_m, nlist,
     ix.close()
 
 
+@pytest.mark.parametrize("dim,pq_m,nlist,nprobe", [
+    (96, 24, 4096, 256),   # 1024 re-score slots: one workgroup per CU, wide instance
+    (96, 24, 2048, 256),   # the same LDS, chunks too short for its batches: sixteen waves
+    (768, 96, 2048, 32),   # query rows in LDS: wide instance with LDS operands
+])
+def test_probe_one_workgroup_per_cu_large_batch(ovvs, res, tmp_path, dim, pq_m, nlist, nprobe):
+    """Batches of at least 256 workgroups at shapes whose LDS admits one workgroup per
+    CU take the sixteen-wave instances (deeper prefetch where the chunks allow)."""
+    rng = np.random.default_rng(dim + nlist + nprobe)
+    centers = rng.standard_normal((256, dim)).astype(np.float32)
+    data = _mixture(rng, 30000, dim, centers)
+    q = _mixture(rng, 4200, dim, centers)
+    say("build", dict(dim=dim, pq_m=pq_m, nlist=nlist, nprobe=nprobe))
+    ix = ovvs.neighbors.ivf_pq.build(data, nlist=nlist, pq_m=pq_m, pq_nbits=8, resources=res)
+    p = tmp_path / "probe_wide.ipq1"
+    ix.serialize(p)
+    orc = Oracle(read_ipq1(p))
+    _check(ix, orc, q, 10, nprobe, 32, f"wide d{dim} l{nlist} p{nprobe}")
+    ix.close()
+
+
 def test_probe_fallback_for_tied_centroids(ovvs, res, tmp_path):
     """700 identical centroids tie every approximate score near them, so queries
     there have more candidates than the re-score capacity and are ranked by the
